@@ -1,0 +1,355 @@
+// extern "C" boundary of libhcp_mi355x.so: argument validation, host-side
+// planners and kernel launches.  Declarations and their reference citations
+// are in include/hcp_mi355x.h.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <numeric>
+#include <vector>
+
+#include "params.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return HCP_OK;
+  return fail(HCP_ELAUNCH, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
+}
+
+bool dtype16(int32_t d) { return d == HCP_DTYPE_F16 || d == HCP_DTYPE_BF16; }
+
+int check_heads(int32_t h, int32_t hkv, int32_t d, int32_t dtype, const char* who) {
+  if (h <= 0 || hkv <= 0) return fail(HCP_EINVAL, "%s: num_heads/num_kv_heads must be > 0", who);
+  if (h % hkv != 0)
+    return fail(HCP_EINVAL, "%s: num_heads (%d) not a multiple of num_kv_heads (%d)", who, h, hkv);
+  if (d != 64 && d != 128)
+    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d not supported (64 or 128)", who, d);
+  if (!dtype16(dtype)) return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
+  return HCP_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; }
+
+int check_segment(const hcp_kv_segment& s, int32_t hd, const char* who, int idx) {
+  if (s.len < 0 || s.start < 0) return fail(HCP_EINVAL, "%s: entry %d: negative kv start/len", who, idx);
+  if (s.len > 0 && (s.k_addr == 0 || s.v_addr == 0))
+    return fail(HCP_EINVAL, "%s: entry %d: null k/v address", who, idx);
+  if ((s.k_addr & 15) || (s.v_addr & 15))
+    return fail(HCP_EINVAL, "%s: entry %d: k/v address not 16-byte aligned", who, idx);
+  if ((s.stride_tok % 8) || (s.stride_head % 8) || (s.block_table && (s.stride_block % 8)))
+    return fail(HCP_EINVAL, "%s: entry %d: kv strides must be multiples of 8 elements", who, idx);
+  if (s.block_table) {
+    if (s.block_size <= 0 || (s.block_size & (s.block_size - 1)))
+      return fail(HCP_EINVAL, "%s: entry %d: block_size %d not a power of two", who, idx,
+                  s.block_size);
+  }
+  (void)hd;
+  return HCP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hcp_abi_version(void) { return HCP_ABI_VERSION; }
+
+const char* hcp_last_error(void) { return g_err; }
+
+int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, float* lse,
+                     int64_t tq, int64_t tk, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int64_t q_stride_tok, int64_t q_stride_head,
+                     int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
+                     int64_t v_stride_head, int64_t o_stride_tok, int64_t o_stride_head,
+                     int64_t lse_stride_head, float scale, int32_t causal,
+                     int64_t causal_offset, int32_t dtype, void* stream) {
+  const char* who = "hcp_attn_fwd_lse";
+  int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
+  if (rc) return rc;
+  if (tq < 0 || tk < 0) return fail(HCP_EINVAL, "%s: negative tq/tk", who);
+  if (tq == 0) return HCP_OK;
+  if (!q || !out || !lse) return fail(HCP_EINVAL, "%s: null q/out/lse", who);
+  if (tk > 0 && (!k || !v)) return fail(HCP_EINVAL, "%s: null k/v", who);
+  if (!aligned16(q) || !aligned16(out) || (tk > 0 && (!aligned16(k) || !aligned16(v))))
+    return fail(HCP_EINVAL, "%s: q/k/v/out must be 16-byte aligned", who);
+  if ((q_stride_tok | q_stride_head | k_stride_tok | k_stride_head | v_stride_tok |
+       v_stride_head | o_stride_tok | o_stride_head) % 8)
+    return fail(HCP_EINVAL, "%s: strides must be multiples of 8 elements", who);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(HCP_EINVAL, "%s: scale must be finite and > 0", who);
+  if (tq > (int64_t)INT32_MAX * 64) return fail(HCP_EINVAL, "%s: tq too large", who);
+
+  hcp::FwdParams p{};
+  p.q = q;
+  p.q_stride_tok = q_stride_tok;
+  p.q_stride_head = q_stride_head;
+  p.out = out;
+  p.o_stride_tok = o_stride_tok;
+  p.o_stride_head = o_stride_head;
+  p.lse = lse;
+  p.lse_stride_head = lse_stride_head;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.scale_log2 = scale * hcp::kLog2e;
+  p.num_tiles = static_cast<int32_t>((tq + hcp::kFwdBM - 1) / hcp::kFwdBM);
+  p.single.q_start = 0;
+  p.single.q_len = tq;
+  p.single.causal_offset = causal ? causal_offset : 0;
+  p.single.kv.k_addr = reinterpret_cast<uint64_t>(k);
+  p.single.kv.v_addr = reinterpret_cast<uint64_t>(v);
+  p.single.kv.stride_tok = k_stride_tok;
+  p.single.kv.stride_head = k_stride_head;
+  p.single.kv.len = tk;
+  if (k_stride_tok != v_stride_tok || k_stride_head != v_stride_head)
+    return fail(HCP_EUNSUPPORTED, "%s: k and v must share strides", who);
+  hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, false, false,
+                                 static_cast<hipStream_t>(stream));
+  return launch_status(e, who);
+}
+
+int hcp_varlen_block_m(int32_t head_dim, int32_t dtype) {
+  (void)head_dim;
+  (void)dtype;
+  return hcp::kFwdBM;
+}
+
+int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries, int32_t causal,
+                          int32_t block_m, int32_t* tiles_out, int32_t cap) {
+  const char* who = "hcp_plan_varlen_tiles";
+  if (num_entries < 0 || block_m <= 0) return fail(HCP_EINVAL, "%s: bad sizes", who);
+  if (num_entries > 0 && !entries) return fail(HCP_EINVAL, "%s: null entries", who);
+  struct T {
+    int64_t cost;
+    int32_t e, qb;
+  };
+  std::vector<T> v;
+  for (int32_t i = 0; i < num_entries; ++i) {
+    const hcp_varlen_entry& en = entries[i];
+    if (en.q_len < 0 || en.kv.len < 0) return fail(HCP_EINVAL, "%s: entry %d negative", who, i);
+    const int64_t nqb = (en.q_len + block_m - 1) / block_m;
+    for (int64_t b = 0; b < nqb; ++b) {
+      int64_t keys = en.kv.len;
+      if (causal) {
+        const int64_t lim = en.causal_offset + (b + 1) * block_m;
+        keys = std::max<int64_t>(0, std::min(keys, lim));
+      }
+      v.push_back({keys, i, static_cast<int32_t>(b)});
+    }
+  }
+  if (static_cast<int64_t>(v.size()) > INT32_MAX) return fail(HCP_EINVAL, "%s: too many tiles", who);
+  const int32_t n = static_cast<int32_t>(v.size());
+  if (n > cap || (n > 0 && !tiles_out))
+    return fail(HCP_EWORKSPACE, "%s: need %d tiles, cap %d", who, n, cap);
+  // longest processing time first; ties keep (entry, block) order
+  std::stable_sort(v.begin(), v.end(), [](const T& a, const T& b) { return a.cost > b.cost; });
+  for (int32_t i = 0; i < n; ++i) {
+    tiles_out[2 * i] = v[i].e;
+    tiles_out[2 * i + 1] = v[i].qb;
+  }
+  return n;
+}
+
+int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok, int64_t q_stride_head, void* out,
+                        int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+                        int64_t lse_stride_head, const hcp_varlen_entry* entries,
+                        int32_t num_entries, const int32_t* tiles, int32_t num_tiles,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                        int32_t causal, int32_t paged, int32_t dtype, void* stream) {
+  const char* who = "hcp_attn_fwd_varlen";
+  int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
+  if (rc) return rc;
+  if (num_entries < 0 || num_tiles < 0) return fail(HCP_EINVAL, "%s: negative counts", who);
+  if (num_tiles == 0) return HCP_OK;
+  if (!q || !out || !lse || !entries || !tiles) return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (!aligned16(q) || !aligned16(out)) return fail(HCP_EINVAL, "%s: q/out not 16-byte aligned", who);
+  if ((q_stride_tok | q_stride_head | o_stride_tok | o_stride_head) % 8)
+    return fail(HCP_EINVAL, "%s: strides must be multiples of 8 elements", who);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(HCP_EINVAL, "%s: scale must be finite and > 0", who);
+  hcp::FwdParams p{};
+  p.q = q;
+  p.q_stride_tok = q_stride_tok;
+  p.q_stride_head = q_stride_head;
+  p.out = out;
+  p.o_stride_tok = o_stride_tok;
+  p.o_stride_head = o_stride_head;
+  p.lse = lse;
+  p.lse_stride_head = lse_stride_head;
+  p.entries = entries;
+  p.tiles = tiles;
+  p.num_tiles = num_tiles;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.scale_log2 = scale * hcp::kLog2e;
+  hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, paged != 0, true,
+                                 static_cast<hipStream_t>(stream));
+  return launch_status(e, who);
+}
+
+int hcp_plan_decode_splits(const hcp_varlen_entry* entries, int32_t num_entries,
+                           const int32_t* entry_seq, int32_t num_seqs, int32_t causal,
+                           int32_t split_tokens, hcp_decode_split* splits_out, int32_t cap,
+                           int32_t* seq_partial_start) {
+  const char* who = "hcp_plan_decode_splits";
+  if (num_entries < 0 || num_seqs < 0 || split_tokens <= 0)
+    return fail(HCP_EINVAL, "%s: bad sizes", who);
+  if ((num_entries > 0 && (!entries || !entry_seq)) || !seq_partial_start)
+    return fail(HCP_EINVAL, "%s: null pointer", who);
+  int32_t n = 0;
+  int32_t cur = 0;
+  seq_partial_start[0] = 0;
+  for (int32_t i = 0; i < num_entries; ++i) {
+    const int32_t s = entry_seq[i];
+    if (s < 0 || s >= num_seqs || s < cur)
+      return fail(HCP_EINVAL, "%s: entry %d: sequence %d out of order/range", who, i, s);
+    if (entries[i].q_len != 1)
+      return fail(HCP_EINVAL, "%s: entry %d: q_len must be 1 for decode", who, i);
+    if (entries[i].kv.len < 0 || entries[i].kv.len > INT32_MAX)
+      return fail(HCP_EINVAL, "%s: entry %d: kv len out of range", who, i);
+    while (cur < s) seq_partial_start[++cur] = n;
+    int64_t len = entries[i].kv.len;
+    if (causal) len = std::max<int64_t>(0, std::min<int64_t>(len, entries[i].causal_offset + 1));
+    for (int64_t b = 0; b < len; b += split_tokens) {
+      if (n >= cap || !splits_out) return fail(HCP_EWORKSPACE, "%s: split cap %d exceeded", who, cap);
+      splits_out[n].entry = i;
+      splits_out[n].key_begin = static_cast<int32_t>(b);
+      splits_out[n].key_end = static_cast<int32_t>(std::min<int64_t>(len, b + split_tokens));
+      splits_out[n].reserved = 0;
+      ++n;
+    }
+  }
+  while (cur < num_seqs) seq_partial_start[++cur] = n;
+  return n;
+}
+
+size_t hcp_decode_workspace_bytes(int32_t num_splits, int32_t num_heads, int32_t head_dim) {
+  if (num_splits <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  const size_t n = static_cast<size_t>(num_splits) * num_heads;
+  const size_t o = n * head_dim * sizeof(float);
+  const size_t o_al = (o + 255) & ~static_cast<size_t>(255);
+  return o_al + n * sizeof(float);
+}
+
+int hcp_decode_splitkv(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                       const hcp_varlen_entry* entries, int32_t num_entries,
+                       const hcp_decode_split* splits, int32_t num_splits,
+                       const int32_t* seq_partial_start, int32_t num_seqs, void* workspace,
+                       size_t workspace_bytes, void* out, int64_t o_stride_tok,
+                       int64_t o_stride_head, float* lse, int64_t lse_stride_head,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                       int32_t dtype, void* stream) {
+  const char* who = "hcp_decode_splitkv";
+  int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
+  if (rc) return rc;
+  if (num_heads / num_kv_heads > 16)
+    return fail(HCP_EUNSUPPORTED, "%s: more than 16 query heads per KV head", who);
+  if (num_entries < 0 || num_splits < 0 || num_seqs < 0)
+    return fail(HCP_EINVAL, "%s: negative counts", who);
+  if (num_seqs == 0) return HCP_OK;
+  if (!q || !out || !seq_partial_start || (num_splits > 0 && (!entries || !splits)))
+    return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (!aligned16(q)) return fail(HCP_EINVAL, "%s: q not 16-byte aligned", who);
+  if ((q_stride_tok | q_stride_head) % 8)
+    return fail(HCP_EINVAL, "%s: q strides must be multiples of 8 elements", who);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(HCP_EINVAL, "%s: scale must be finite and > 0", who);
+  const size_t need = hcp_decode_workspace_bytes(num_splits, num_heads, head_dim);
+  if (num_splits > 0 && (!workspace || workspace_bytes < need))
+    return fail(HCP_EWORKSPACE, "%s: workspace %zu bytes < %zu needed", who, workspace_bytes, need);
+  if (workspace && !aligned16(workspace))
+    return fail(HCP_EINVAL, "%s: workspace not 16-byte aligned", who);
+  const size_t n = static_cast<size_t>(num_splits) * num_heads;
+  const size_t o_al = (n * head_dim * sizeof(float) + 255) & ~static_cast<size_t>(255);
+  hcp::DecParams dp{};
+  dp.q = q;
+  dp.q_stride_tok = q_stride_tok;
+  dp.q_stride_head = q_stride_head;
+  dp.entries = entries;
+  dp.splits = splits;
+  dp.num_splits = num_splits;
+  dp.ws_o = static_cast<float*>(workspace);
+  dp.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_al);
+  dp.num_heads = num_heads;
+  dp.num_kv_heads = num_kv_heads;
+  dp.group = num_heads / num_kv_heads;
+  dp.scale_log2 = scale * hcp::kLog2e;
+  hcp::RedParams rp{};
+  rp.ws_o = dp.ws_o;
+  rp.ws_lse = dp.ws_lse;
+  rp.seq_partial_start = seq_partial_start;
+  rp.num_seqs = num_seqs;
+  rp.out = out;
+  rp.o_stride_tok = o_stride_tok;
+  rp.o_stride_head = o_stride_head;
+  rp.lse = lse;
+  rp.lse_stride_head = lse_stride_head;
+  rp.num_heads = num_heads;
+  hipError_t e = hcp::launch_decode(dp, rp, head_dim, dtype, static_cast<hipStream_t>(stream));
+  return launch_status(e, who);
+}
+
+int hcp_merge_attn_states(void* out, int64_t o_stride_tok, int64_t o_stride_head,
+                          int32_t out_dtype, float* out_lse, int64_t out_lse_stride_head,
+                          const void* prefix_out, int64_t p_stride_tok, int64_t p_stride_head,
+                          int32_t prefix_dtype, const float* prefix_lse,
+                          int64_t p_lse_stride_head, const void* suffix_out,
+                          int64_t s_stride_tok, int64_t s_stride_head, int32_t suffix_dtype,
+                          const float* suffix_lse, int64_t s_lse_stride_head,
+                          int64_t num_tokens, int32_t num_heads, int32_t head_dim,
+                          void* stream) {
+  const char* who = "hcp_merge_attn_states";
+  if (num_tokens < 0 || num_heads <= 0 || head_dim <= 0)
+    return fail(HCP_EINVAL, "%s: bad sizes", who);
+  if (head_dim % 8) return fail(HCP_EUNSUPPORTED, "%s: head_dim must be a multiple of 8", who);
+  for (int32_t d : {out_dtype, prefix_dtype, suffix_dtype})
+    if (d != HCP_DTYPE_F16 && d != HCP_DTYPE_BF16 && d != HCP_DTYPE_F32)
+      return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, d);
+  if (num_tokens == 0) return HCP_OK;
+  if (!out || !prefix_out || !suffix_out || !prefix_lse || !suffix_lse)
+    return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (!aligned16(out) || !aligned16(prefix_out) || !aligned16(suffix_out))
+    return fail(HCP_EINVAL, "%s: o tensors must be 16-byte aligned", who);
+  if ((o_stride_tok | o_stride_head | p_stride_tok | p_stride_head | s_stride_tok |
+       s_stride_head) % 8)
+    return fail(HCP_EINVAL, "%s: strides must be multiples of 8 elements", who);
+  if (num_tokens * num_heads * (head_dim / 8) > (int64_t)INT32_MAX * 256)
+    return fail(HCP_EINVAL, "%s: too large", who);
+  hcp::MergeParams p{};
+  p.out = out;
+  p.o_stride_tok = o_stride_tok;
+  p.o_stride_head = o_stride_head;
+  p.out_lse = out_lse;
+  p.out_lse_stride = out_lse_stride_head;
+  p.po = prefix_out;
+  p.p_stride_tok = p_stride_tok;
+  p.p_stride_head = p_stride_head;
+  p.plse = prefix_lse;
+  p.p_lse_stride = p_lse_stride_head;
+  p.so = suffix_out;
+  p.s_stride_tok = s_stride_tok;
+  p.s_stride_head = s_stride_head;
+  p.slse = suffix_lse;
+  p.s_lse_stride = s_lse_stride_head;
+  p.num_tokens = num_tokens;
+  p.num_heads = num_heads;
+  p.head_dim = head_dim;
+  p.out_dtype = out_dtype;
+  p.p_dtype = prefix_dtype;
+  p.s_dtype = suffix_dtype;
+  return launch_status(hcp::launch_merge(p, static_cast<hipStream_t>(stream)), who);
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// Kernel parameter blocks and launch functions shared between the kernel
+// translation units and the extern "C" layer (abi.hip).
+#pragma once
+
+#include "common.h"
+
+namespace hcp {
+
+constexpr int kFwdBM = 128;  // query rows per prefill workgroup
+constexpr int kFwdBN = 64;   // keys per prefill tile
+constexpr int kFwdThreads = 256;
+
+struct FwdParams {
+  const void* q;
+  int64_t q_stride_tok, q_stride_head;
+  void* out;
+  int64_t o_stride_tok, o_stride_head;
+  float* lse;
+  int64_t lse_stride_head;
+  const hcp_varlen_entry* entries;  // varlen: device array
+  const int32_t* tiles;             // varlen: device (entry, q_block) pairs
+  int32_t num_tiles;                // varlen: tiles; else query blocks
+  int32_t num_heads, num_kv_heads, group;
+  float scale_log2;
+  hcp_varlen_entry single;  // non-varlen: the one entry
+};
+
+struct DecParams {
+  const void* q;
+  int64_t q_stride_tok, q_stride_head;
+  const hcp_varlen_entry* entries;
+  const hcp_decode_split* splits;
+  int32_t num_splits;
+  float* ws_o;    // [num_splits, H, D]
+  float* ws_lse;  // [num_splits, H]
+  int32_t num_heads, num_kv_heads, group;
+  float scale_log2;
+};
+
+struct RedParams {
+  const float* ws_o;
+  const float* ws_lse;
+  const int32_t* seq_partial_start;
+  int32_t num_seqs;
+  void* out;
+  int64_t o_stride_tok, o_stride_head;
+  float* lse;
+  int64_t lse_stride_head;
+  int32_t num_heads;
+};
+
+struct MergeParams {
+  void* out;
+  int64_t o_stride_tok, o_stride_head;
+  float* out_lse;
+  int64_t out_lse_stride;
+  const void* po;
+  int64_t p_stride_tok, p_stride_head;
+  const float* plse;
+  int64_t p_lse_stride;
+  const void* so;
+  int64_t s_stride_tok, s_stride_head;
+  const float* slse;
+  int64_t s_lse_stride;
+  int64_t num_tokens;
+  int32_t num_heads, head_dim;
+  int32_t out_dtype, p_dtype, s_dtype;
+};
+
+hipError_t launch_fwd(const FwdParams& p, int head_dim, int dtype, bool causal,
+                      bool paged, bool varlen, hipStream_t st);
+hipError_t launch_decode(const DecParams& dp, const RedParams& rp, int head_dim,
+                         int dtype, hipStream_t st);
+hipError_t launch_merge(const MergeParams& p, hipStream_t st);
+
+}  // namespace hcp

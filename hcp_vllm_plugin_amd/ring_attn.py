@@ -1,0 +1,85 @@
+"""Flash attention with LSE on the HIP kernels (the ``ring_attn_with_lse`` contract).
+
+Mirrors hcp_vllm_plugin/ring_triton_attn.py:155-207: the same call
+``ring_attn_with_lse(q, k, v, scale, causal_offset) -> (out, lse)``, the same
+shapes (q ``[Tq, H, D]``, k/v ``[Tk, Hkv, D]``, out ``[Tq, H, D]`` in q.dtype,
+lse ``[H, Tq]`` float32 natural log), ``causal_offset=None`` meaning
+non-causal and an integer meaning causal with query 0 at that position in the
+KV frame.  The work runs in ``hcp_attn_fwd_lse`` (libhcp_mi355x.so).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = ["ring_attn_with_lse", "check_qkv"]
+
+
+def check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Shape/dtype/device checks of the kernel contract (ring_triton_attn.py:169-172)."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q, k, v must be 3-D: [T, heads, head_dim]")
+    if k.shape != v.shape:
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    if q.shape[2] != k.shape[2]:
+        raise ValueError("q and k head_dim differ")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError(f"num_heads {q.shape[1]} not a multiple of num_kv_heads {k.shape[1]}")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q/k/v must share dtype float16 or bfloat16, got {q.dtype}/{k.dtype}/{v.dtype}")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("q, k, v must be GPU tensors")
+    if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("head_dim must be the contiguous dimension")
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Return t, or a contiguous copy when its layout is not kernel-loadable."""
+    ok = (
+        t.data_ptr() % 16 == 0
+        and all(s % 8 == 0 for s in t.stride()[:-1])
+        and t.stride(-1) == 1
+    )
+    return t if ok else t.contiguous()
+
+
+def ring_attn_with_lse(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    causal_offset: int | None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Flash-style attention with LSE output (HIP, gfx950).
+
+    causal_offset: absolute position of query token 0 within the KV range
+    (None => non-causal, all keys visible).  Returns (out ``[Tq, H, D]`` in
+    q.dtype, lse ``[H, Tq]`` float32 natural log).  A query with no visible
+    key (empty KV, or a negative offset) gets out 0 and lse -inf.
+    """
+    check_qkv(q, k, v)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    tq, num_heads, head_dim = q.shape
+    tk, num_kv_heads = k.shape[0], k.shape[1]
+    out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((num_heads, tq), dtype=torch.float32, device=q.device)
+    if tq == 0:
+        return out, lse
+    if k.stride() != v.stride():
+        v = v.contiguous()
+        k = k.contiguous()
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        rc = L.hcp_attn_fwd_lse(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            tq, tk, num_heads, num_kv_heads, head_dim,
+            q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+            v.stride(0), v.stride(1), out.stride(0), out.stride(1), lse.stride(0),
+            float(scale), 0 if causal_offset is None else 1,
+            0 if causal_offset is None else int(causal_offset),
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
+        )
+    _lib.check(rc, "hcp_attn_fwd_lse")
+    return out, lse

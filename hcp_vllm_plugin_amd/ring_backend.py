@@ -1,0 +1,474 @@
+"""HCP ring-attention backend on the MI355X HIP kernels.
+
+Drop-in for hcp_vllm_plugin/ring_backend.py's hot path:
+
+* ``HcpRingAttentionBackend`` -- ``get_name() == "CUSTOM"``, ``get_impl_cls``,
+  ``get_builder_cls``, ``forward_includes_kv_cache_update = False``
+  (ring_backend.py:427-449).  When vLLM is importable it subclasses vLLM's
+  ``FlashAttentionBackend`` exactly as the reference does (ring_backend.py:71-74);
+  without vLLM it is a plain class with the same static methods.
+* ``HcpRingAttentionImpl`` -- ``__init__`` (ring_backend.py:464-498) and
+  ``forward(layer, query, key, value, kv_cache, attn_metadata, output,
+  output_scale=None, output_block_scale=None)`` (ring_backend.py:576-834) with
+  the reference's segmentation: vanilla causal attention when a request has no
+  peer, plain causal attention for the ``n_a`` queries inside the peer region,
+  and for the rest local causal attention over ``[peer_end, tk)`` at offset
+  ``qpos0 + n_a - peer_end`` merged with non-causal attention over the peer.
+  Instead of a Python loop with a gather copy and 5-6 launches per request,
+  a whole batch runs as one varlen launch over the paged cache (read in
+  place), one launch over the staged peer KV and one merge; a pure decode
+  batch runs the split-KV decode kernel.
+* ``_attn`` / ``_merge`` (ring_backend.py:309-360) with ``HCP_RING_IMPL`` /
+  ``HCP_RING_MERGE`` read on every call.  ``hip`` is the default; ``triton``
+  is accepted as an alias so existing launch scripts keep working.  There is
+  no torch fallback in this package: ``torch`` raises, and a kernel error
+  raises instead of silently switching paths.
+* The peer-KV staging input contract (ring_backend.py:78-136):
+  ``PEER_KV_STAGING[(chunk_key, layer_name)] = (k, v)`` with k/v
+  ``[n, Hkv, D]`` post-RoPE, ``PEER_REQ_MAP[first_block_id] = [chunk keys]``.
+* ``IMPL_STATS`` evidence counters (ring_backend.py:295-306).  ``attn_hip`` /
+  ``merge_hip`` count kernel launches; the legacy keys ``attn_triton`` /
+  ``merge_triton`` mirror them so validators that read those names still see
+  which path ran, and ``attn_torch`` / ``merge_torch`` stay 0.
+"""
+
+from __future__ import annotations
+
+import enum
+import logging
+import os
+
+import torch
+
+from . import _lib
+from .merge import merge_attn_states
+from .ring_attn import ring_attn_with_lse
+from .varlen import (
+    DecodeBatch,
+    PagedCache,
+    VarlenLaunch,
+    make_entry,
+    segment_contiguous,
+    segment_paged,
+)
+
+logger = logging.getLogger(__name__)
+
+try:  # optional: the real vLLM base classes, as the reference uses them
+    from vllm.v1.attention.backend import AttentionImpl as _ImplBase  # type: ignore
+    from vllm.v1.attention.backend import AttentionType  # type: ignore
+    from vllm.v1.attention.backends.flash_attn import (  # type: ignore
+        FlashAttentionBackend as _BackendBase,
+        FlashAttentionMetadataBuilder as _BuilderCls,
+    )
+
+    HAVE_VLLM = True
+except ImportError:  # vLLM absent: same surface, no base classes
+    HAVE_VLLM = False
+    _ImplBase = object
+    _BackendBase = object
+    _BuilderCls = None
+
+    class AttentionType(str, enum.Enum):  # type: ignore[no-redef]
+        DECODER = "decoder"
+        ENCODER = "encoder"
+        ENCODER_ONLY = "encoder_only"
+        ENCODER_DECODER = "encoder_decoder"
+
+
+# ---------------------------------------------------------------------------
+# Peer KV staging (input contract; the connector writes, forward reads)
+# ---------------------------------------------------------------------------
+PEER_KV_STAGING: dict[tuple[str, str], tuple[torch.Tensor, torch.Tensor]] = {}
+PEER_REQ_MAP: dict[int, list[str]] = {}
+
+
+def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Stage a peer chunk's K/V ``[n, Hkv, D]`` (post-RoPE) for one layer."""
+    PEER_KV_STAGING[(chunk_key, layer_name)] = (k, v)
+
+
+def drop_chunk_kv(chunk_key: str) -> int:
+    keys = [key for key in PEER_KV_STAGING if key[0] == chunk_key]
+    for key in keys:
+        del PEER_KV_STAGING[key]
+    return len(keys)
+
+
+def map_request_peer(first_block_id: int, chunk_keys) -> None:
+    """Bind a request (by its first block id) to its ordered prefix chunks."""
+    if isinstance(chunk_keys, str):
+        chunk_keys = [chunk_keys]
+    PEER_REQ_MAP[first_block_id] = list(chunk_keys)
+
+
+def unmap_request_peer(first_block_id: int) -> None:
+    PEER_REQ_MAP.pop(first_block_id, None)
+
+
+def request_peer_chunk(first_block_id: int) -> list[str] | None:
+    return PEER_REQ_MAP.get(first_block_id)
+
+
+def clear_peer_kv() -> None:
+    PEER_KV_STAGING.clear()
+    PEER_REQ_MAP.clear()
+
+
+# ---------------------------------------------------------------------------
+# Switches and evidence counters
+# ---------------------------------------------------------------------------
+BATCH_STATS: dict = {"max_reqs": 0}
+
+IMPL_STATS: dict = {
+    "attn_hip": 0,
+    "merge_hip": 0,
+    "decode_hip": 0,
+    "attn_triton": 0,
+    "merge_triton": 0,
+    "attn_torch": 0,
+    "merge_torch": 0,
+}
+
+_FAST_IMPLS = ("hip", "triton")
+
+
+def reset_impl_stats() -> None:
+    for key in IMPL_STATS:
+        IMPL_STATS[key] = 0
+
+
+def reset_batch_stats() -> None:
+    BATCH_STATS["max_reqs"] = 0
+
+
+def _ring_enabled() -> bool:
+    return os.environ.get("HCP_RING_ENABLED", "1") == "1"
+
+
+def _split_tokens() -> int:
+    return int(os.environ.get("HCP_RING_SPLIT_TOKENS", "0"))
+
+
+def _ring_impl() -> str:
+    return os.environ.get("HCP_RING_IMPL", "hip")
+
+
+def _merge_impl() -> str:
+    return os.environ.get("HCP_RING_MERGE", "hip")
+
+
+def _require_fast(kind: str, value: str) -> None:
+    if value not in _FAST_IMPLS:
+        raise NotImplementedError(
+            f"{kind}={value!r}: this build runs the HIP kernels only "
+            f"(accepted: {', '.join(_FAST_IMPLS)}); there is no torch path"
+        )
+
+
+def _count(kind: str, n: int = 1) -> None:
+    IMPL_STATS[f"{kind}_hip"] += n
+    legacy = f"{kind}_triton"
+    if legacy in IMPL_STATS:
+        IMPL_STATS[legacy] += n
+
+
+def _attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    q_pos0_in_kv: int | None,
+    window: int | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Attention + LSE on the HIP kernel (ring_backend.py:309-336 contract).
+
+    Returns (out ``[Tq, H, D]`` in q.dtype, lse ``[H, Tq]`` float32).
+    """
+    _require_fast("HCP_RING_IMPL", _ring_impl())
+    if window is not None:
+        raise NotImplementedError("sliding-window attention is not built for the HIP path")
+    o, lse = ring_attn_with_lse(q, k, v, scale, q_pos0_in_kv)
+    _count("attn")
+    return o, lse
+
+
+def _merge(
+    o_loc: torch.Tensor, lse_loc: torch.Tensor, o_peer: torch.Tensor, lse_peer: torch.Tensor
+) -> torch.Tensor:
+    """Local + peer LSE merge on the HIP kernel (ring_backend.py:339-360).
+
+    Same argument order as the reference: ``merge_attn_states(out, o_peer,
+    lse_peer, o_loc, lse_loc)`` with out in ``o_loc.dtype``.
+    """
+    _require_fast("HCP_RING_MERGE", _merge_impl())
+    out = torch.empty_like(o_loc, memory_format=torch.contiguous_format)
+    merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc)
+    _count("merge")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Backend class (registered as CUSTOM)
+# ---------------------------------------------------------------------------
+class HcpRingAttentionBackend(_BackendBase):  # type: ignore[misc,valid-type]
+    """Ring-attention backend: FlashAttention cache layout + metadata builder
+    (inherited when vLLM is present), HIP attention impl with LSE peer merge.
+
+    ``get_name()`` stays "CUSTOM": vLLM's Attention layer looks the backend up
+    by that enum member (ring_backend.py:439-441).
+    """
+
+    forward_includes_kv_cache_update: bool = False
+
+    @staticmethod
+    def get_name() -> str:
+        return "CUSTOM"
+
+    @staticmethod
+    def get_impl_cls() -> type["HcpRingAttentionImpl"]:
+        return HcpRingAttentionImpl
+
+    @staticmethod
+    def get_builder_cls():
+        return _BuilderCls
+
+
+class _Plan:
+    """Launch descriptors for one forward call."""
+
+    def __init__(self):
+        self.local: list = []           # causal entries over the paged cache
+        self.peer_rounds: list = []     # per round: {"contig": [...], "paged": [...]}
+        self.any_peer = False
+
+
+class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
+    """HIP attention + LSE merge with peer chunk KV (ring_backend.py:452-834).
+
+    Reads the paged cache in either vLLM 0.31 ``[nb, Hkv, bs, 2*D]`` or vLLM
+    0.23 ``[nb, 2, bs, Hkv, D]`` layout, in place.  Peer KV is consumed from
+    the staging dict (or from a split of the local cache) and never written.
+    """
+
+    def __init__(
+        self,
+        num_heads: int,
+        head_size: int,
+        scale: float,
+        num_kv_heads: int | None = None,
+        alibi_slopes: list[float] | None = None,
+        sliding_window: int | None = None,
+        kv_cache_dtype: str = "auto",
+        logits_soft_cap: float | None = None,
+        attn_type=AttentionType.DECODER,
+        kv_sharing_target_layer_name: str | None = None,
+        **kwargs,
+    ) -> None:
+        self.num_heads = num_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.num_kv_heads = num_kv_heads if num_kv_heads is not None else num_heads
+        self.kv_cache_dtype = kv_cache_dtype
+        self.attn_type = attn_type
+        self.kv_sharing_target_layer_name = kv_sharing_target_layer_name
+        self.supports_quant_query_input = False
+        if alibi_slopes is not None:
+            raise NotImplementedError("HCP ring backend: ALiBi not supported")
+        if logits_soft_cap:
+            raise NotImplementedError("HCP ring backend: soft cap not supported")
+        if sliding_window is not None:
+            raise NotImplementedError("HCP ring backend (HIP): sliding window not supported")
+        if kv_cache_dtype not in ("auto", "float16", "bfloat16"):
+            raise NotImplementedError(f"kv_cache_dtype {kv_cache_dtype} not supported")
+        self.sliding_window = sliding_window
+        self.num_queries_per_kv = self.num_heads // self.num_kv_heads
+
+    # -- paged KV write (the step before the path) ----------------------------
+    def do_kv_cache_update(
+        self,
+        layer,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        kv_cache: torch.Tensor,
+        slot_mapping: torch.Tensor,
+    ) -> None:
+        """Write this step's K/V into the paged cache at ``slot_mapping``.
+
+        ring_backend.py:501-539 (without the decode-ring skip, whose ring
+        transport is not part of this build).  slot = block * bs + offset.
+        """
+        if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
+            return
+        n = slot_mapping.shape[0]
+        pc = PagedCache.from_tensor(kv_cache)
+        slot = slot_mapping.long()
+        blk = torch.div(slot, pc.block_size, rounding_mode="floor")
+        off = slot % pc.block_size
+        d = pc.head_dim
+        if pc.layout == "v031":
+            kv_cache[blk, :, off, :d] = key[:n]
+            kv_cache[blk, :, off, d:] = value[:n]
+        else:
+            kv_cache[blk, 0, off] = key[:n]
+            kv_cache[blk, 1, off] = value[:n]
+
+    # -- planning -------------------------------------------------------------
+    def _peer_for_request(self, first_block: int, layer_name: str, n_reqs: int):
+        """Ordered staged (k, v) chunks of a request, or None (ring_backend.py:738-772)."""
+        ck_list = PEER_REQ_MAP.get(first_block)
+        if ck_list is None and n_reqs == 1:
+            chunks = {key[0] for key in PEER_KV_STAGING}
+            if len(chunks) == 1:
+                ck_list = [next(iter(chunks))]
+        if not ck_list:
+            return None
+        parts = []
+        for ck in ck_list:
+            kv = PEER_KV_STAGING.get((ck, layer_name))
+            if kv is None:
+                logger.warning(
+                    "HCP ring: request mapped to chunks %s but staging incomplete at layer %s; "
+                    "falling back to local path", ck_list, layer_name)
+                return None
+            parts.append(kv)
+        return parts
+
+    def _plan(self, layer_name, qsl, seq_lens, block_table, first_blocks, pc, split):
+        plan = _Plan()
+        for r in range(len(seq_lens)):
+            qs, qe = qsl[r], qsl[r + 1]
+            tq, tk = qe - qs, seq_lens[r]
+            if tq == 0:
+                continue
+            row = block_table[r]
+            qpos0 = tk - tq
+            staged = None
+            if _ring_enabled():
+                staged = self._peer_for_request(first_blocks[r], layer_name, len(seq_lens))
+            peer_segs = []
+            if staged is not None:
+                total = sum(int(kv[0].shape[0]) for kv in staged)
+                peer_end = min(total, tk)
+                for kk, vv in staged:
+                    if kk.shape[0] > 0:
+                        peer_segs.append(segment_contiguous(kk, vv))
+            elif split > 0:
+                peer_end = min(split, tk)
+                peer_segs.append(segment_paged(pc, row, 0, peer_end))
+            else:
+                peer_end = 0
+            if peer_end == 0:
+                plan.local.append(make_entry(qs, tq, segment_paged(pc, row, 0, tk), qpos0))
+                continue
+            n_a = max(0, min(tq, peer_end - qpos0))
+            if n_a > 0:
+                plan.local.append(make_entry(qs, n_a, segment_paged(pc, row, 0, tk), qpos0))
+            if n_a < tq:
+                qb0, nb = qs + n_a, tq - n_a
+                plan.local.append(make_entry(
+                    qb0, nb, segment_paged(pc, row, peer_end, tk - peer_end),
+                    qpos0 + n_a - peer_end))
+                for i, seg in enumerate(peer_segs):
+                    while len(plan.peer_rounds) <= i:
+                        plan.peer_rounds.append({"contig": [], "paged": []})
+                    kind = "paged" if seg.block_table else "contig"
+                    plan.peer_rounds[i][kind].append(make_entry(qb0, nb, seg, 0))
+                    plan.any_peer = True
+        return plan
+
+    # -- forward ----------------------------------------------------------------
+    def forward(
+        self,
+        layer,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        kv_cache: torch.Tensor,
+        attn_metadata,
+        output: torch.Tensor,
+        output_scale: torch.Tensor | None = None,
+        output_block_scale: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        if output_scale is not None or output_block_scale is not None:
+            raise NotImplementedError("fused output quant not supported")
+        if attn_metadata is None:
+            return output.fill_(0)  # profiling run
+        if self.attn_type != AttentionType.DECODER:
+            raise NotImplementedError("HCP ring backend supports decoder attention only")
+        _require_fast("HCP_RING_IMPL", _ring_impl())
+        _require_fast("HCP_RING_MERGE", _merge_impl())
+
+        num_actual = attn_metadata.num_actual_tokens
+        query = query[:num_actual]
+        out = output[:num_actual]
+        pc = PagedCache.from_tensor(kv_cache)
+        if pc.num_kv_heads != self.num_kv_heads or pc.head_dim != self.head_size:
+            raise ValueError("kv_cache shape does not match the layer's heads/head_size")
+        # small metadata tensors: one host sync, as the reference (:604-605)
+        qsl = attn_metadata.query_start_loc.tolist()
+        seq_lens = attn_metadata.seq_lens.tolist()
+        block_table = attn_metadata.block_table
+        if block_table.dtype != torch.int32:
+            block_table = block_table.to(torch.int32)
+        block_table = block_table.contiguous()
+        first_blocks = block_table[:, 0].tolist() if block_table.shape[1] > 0 else []
+        BATCH_STATS["max_reqs"] = max(BATCH_STATS["max_reqs"], len(seq_lens))
+        split = _split_tokens() if _ring_enabled() else 0
+        layer_name = getattr(layer, "layer_name", "")
+
+        plan = self._plan(layer_name, qsl, seq_lens, block_table, first_blocks, pc, split)
+        n = len(seq_lens)
+        is_decode = n > 0 and qsl == list(range(n + 1))
+        if is_decode:
+            self._forward_decode(query, out, plan, n)
+        else:
+            self._forward_prefill(query, out, plan)
+        return output
+
+    def _forward_prefill(self, query, out, plan: _Plan) -> None:
+        dev = query.device
+        h = self.num_heads
+        if not plan.any_peer:
+            lse = torch.empty((h, query.shape[0]), dtype=torch.float32, device=dev)
+            VarlenLaunch(plan.local, True, True, dev).run(query, out, lse, self.num_kv_heads,
+                                                         self.scale)
+            _count("attn")
+            return
+        o_loc = torch.empty_like(query, memory_format=torch.contiguous_format)
+        lse_loc = torch.full((h, query.shape[0]), float("-inf"), dtype=torch.float32, device=dev)
+        VarlenLaunch(plan.local, True, True, dev).run(query, o_loc, lse_loc, self.num_kv_heads,
+                                                     self.scale)
+        _count("attn")
+        o_peer = lse_peer = None
+        for rnd in plan.peer_rounds:
+            o_r = torch.empty_like(query, memory_format=torch.contiguous_format)
+            lse_r = torch.full_like(lse_loc, float("-inf"))
+            for kind in ("contig", "paged"):
+                if rnd[kind]:
+                    VarlenLaunch(rnd[kind], False, kind == "paged", dev).run(
+                        query, o_r, lse_r, self.num_kv_heads, self.scale)
+                    _count("attn")
+            if o_peer is None:
+                o_peer, lse_peer = o_r, lse_r
+            else:  # running merge of further prefix chunks (ring_decode.py:46-61)
+                o_m = torch.empty_like(o_peer)
+                lse_m = torch.empty_like(lse_peer)
+                merge_attn_states(o_m, o_peer, lse_peer, o_r, lse_r, lse_m)
+                _count("merge")
+                o_peer, lse_peer = o_m, lse_m
+        # prefix = peer, suffix = local (ring_backend.py:354)
+        merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc)
+        _count("merge")
+
+    def _forward_decode(self, query, out, plan: _Plan, n: int) -> None:
+        segs: list[list] = [[] for _ in range(n)]
+        for e in plan.local:
+            segs[e.q_start].append(e.kv)
+        for rnd in plan.peer_rounds:
+            for kind in ("contig", "paged"):
+                for e in rnd[kind]:
+                    segs[e.q_start].append(e.kv)
+        DecodeBatch(segs, self.num_heads, self.num_kv_heads, self.head_size,
+                    query.device).run(query, out, None, self.scale)
+        _count("decode")

@@ -1,0 +1,327 @@
+"""Batched (varlen) prefill and split-KV decode on the HIP kernels.
+
+The reference runs one flash launch per request and segment and gathers the
+paged local KV into a contiguous copy first (ring_backend.py:611-832,
+:617-624).  This module describes a whole batch as ``hcp_varlen_entry``
+records -- query rows plus a KV segment that is either contiguous (staged
+peer chunks) or paged (the local KV cache, read in place through the block
+table) -- and runs one launch per segment kind:
+
+* ``varlen_attn_with_lse``: causal (local) or non-causal (peer) prefill over
+  every entry, tiles ordered longest-first by ``hcp_plan_varlen_tiles``.
+* ``decode_attn``: split-KV decode of single-token queries; every segment of a
+  sequence (peer and local) is split, and one reduce merges all partials.
+
+Paged layouts (SURVEY of the reference): vLLM 0.31 ``[nb, Hkv, bs, 2*D]`` with
+K in ``[..., :D]`` and V in ``[..., D:]`` (file_connector.py:13-16,175-179),
+and vLLM 0.23 ``[nb, 2, bs, Hkv, D]`` (ring_backend.py:601,617-624).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import DecodeSplit, KvSegment, VarlenEntry
+
+__all__ = [
+    "PagedCache",
+    "segment_contiguous",
+    "segment_paged",
+    "varlen_attn_with_lse",
+    "plan_varlen_tiles",
+    "DecodeBatch",
+    "decode_attn",
+    "choose_split_tokens",
+]
+
+
+@dataclass
+class PagedCache:
+    """A paged KV cache and its element strides.
+
+    ``layout`` is ``"v031"`` for ``[nb, Hkv, bs, 2*D]`` or ``"v023"`` for
+    ``[nb, 2, bs, Hkv, D]``; ``from_tensor`` infers it from the rank.
+    """
+
+    cache: torch.Tensor
+    layout: str
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    k_addr: int
+    v_addr: int
+    stride_tok: int
+    stride_head: int
+    stride_block: int
+
+    @classmethod
+    def from_tensor(cls, cache: torch.Tensor) -> "PagedCache":
+        if cache.stride(-1) != 1:
+            raise ValueError("paged cache: last dim must be contiguous")
+        es = cache.element_size()
+        if cache.dim() == 4:  # [nb, Hkv, bs, 2D]
+            nb, hkv, bs, d2 = cache.shape
+            d = d2 // 2
+            return cls(cache, "v031", hkv, d, bs, cache.data_ptr(),
+                       cache.data_ptr() + d * es,
+                       cache.stride(2), cache.stride(1), cache.stride(0))
+        if cache.dim() == 5 and cache.shape[1] == 2:  # [nb, 2, bs, Hkv, D]
+            nb, _, bs, hkv, d = cache.shape
+            return cls(cache, "v023", hkv, d, bs, cache.data_ptr(),
+                       cache.data_ptr() + cache.stride(1) * es,
+                       cache.stride(2), cache.stride(3), cache.stride(0))
+        raise ValueError(f"unrecognised paged cache shape {tuple(cache.shape)}")
+
+
+def segment_contiguous(k: torch.Tensor, v: torch.Tensor, start: int = 0,
+                       length: int | None = None) -> KvSegment:
+    """Segment over tokens ``[start, start+length)`` of k/v ``[T, Hkv, D]``."""
+    if k.shape != v.shape or k.stride() != v.stride():
+        raise ValueError("k and v must share shape and strides")
+    if k.stride(-1) != 1:
+        raise ValueError("k/v head_dim must be contiguous")
+    n = k.shape[0] - start if length is None else length
+    if start < 0 or n < 0 or start + n > k.shape[0]:
+        raise ValueError("segment out of range")
+    s = KvSegment()
+    s.k_addr = k.data_ptr()
+    s.v_addr = v.data_ptr()
+    s.block_table = 0
+    s.stride_tok = k.stride(0)
+    s.stride_head = k.stride(1)
+    s.stride_block = 0
+    s.start = start
+    s.len = n
+    s.block_size = 0
+    return s
+
+
+def segment_paged(pc: PagedCache, block_table_row: torch.Tensor, start: int,
+                  length: int) -> KvSegment:
+    """Segment over tokens ``[start, start+length)`` of one request's paged KV.
+
+    ``block_table_row`` is the request's int32 block-table row on the device
+    (contiguous); token x lives in block ``row[x // bs]`` at ``x % bs``.
+    """
+    if block_table_row.dtype != torch.int32 or block_table_row.stride(-1) != 1:
+        raise ValueError("block table row must be contiguous int32")
+    nblk = (start + length + pc.block_size - 1) // pc.block_size
+    if length > 0 and nblk > block_table_row.shape[0]:
+        raise ValueError("segment extends past the block-table row")
+    s = KvSegment()
+    s.k_addr = pc.k_addr
+    s.v_addr = pc.v_addr
+    s.block_table = block_table_row.data_ptr()
+    s.stride_tok = pc.stride_tok
+    s.stride_head = pc.stride_head
+    s.stride_block = pc.stride_block
+    s.start = start
+    s.len = length
+    s.block_size = pc.block_size
+    return s
+
+
+def make_entry(q_start: int, q_len: int, seg: KvSegment, causal_offset: int = 0) -> VarlenEntry:
+    e = VarlenEntry()
+    e.q_start = q_start
+    e.q_len = q_len
+    e.causal_offset = causal_offset
+    e.kv = seg
+    return e
+
+
+def _to_device(arr, device: torch.device) -> torch.Tensor:
+    """Copy a ctypes array to a device byte tensor."""
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.to(device)
+
+
+def plan_varlen_tiles(entries: list[VarlenEntry], causal: bool) -> list[tuple[int, int]]:
+    """Host tile plan (entry, q_block), longest first (hcp_plan_varlen_tiles)."""
+    L = _lib.lib()
+    n = len(entries)
+    arr = (VarlenEntry * max(n, 1))(*entries)
+    bm = L.hcp_varlen_block_m(128, _lib.DTYPE_BF16)
+    cap = sum((e.q_len + bm - 1) // bm for e in entries)
+    tiles = (ctypes.c_int32 * max(2 * cap, 2))()
+    rc = L.hcp_plan_varlen_tiles(ctypes.addressof(arr), n, int(causal), bm,
+                                 ctypes.addressof(tiles), cap)
+    _lib.check(rc, "hcp_plan_varlen_tiles")
+    return [(tiles[2 * i], tiles[2 * i + 1]) for i in range(rc)]
+
+
+class VarlenLaunch:
+    """A planned varlen launch: entries and tile list uploaded to the device.
+
+    Build once per batch layout; ``run`` may be called repeatedly (e.g. per
+    layer, or per benchmark step) with any q/out/lse of matching rows.
+    """
+
+    def __init__(self, entries: list[VarlenEntry], causal: bool, paged: bool,
+                 device: torch.device):
+        L = _lib.lib()
+        self.causal = bool(causal)
+        self.paged = bool(paged)
+        self.num_entries = len(entries)
+        for e in entries:
+            if (e.kv.block_table != 0) != self.paged:
+                raise ValueError("all entries of a launch must share the KV form")
+        arr = (VarlenEntry * max(self.num_entries, 1))(*entries)
+        bm = L.hcp_varlen_block_m(128, _lib.DTYPE_BF16)
+        cap = sum((e.q_len + bm - 1) // bm for e in entries)
+        tiles = (ctypes.c_int32 * max(2 * cap, 2))()
+        rc = L.hcp_plan_varlen_tiles(ctypes.addressof(arr), self.num_entries,
+                                     int(self.causal), bm, ctypes.addressof(tiles), cap)
+        _lib.check(rc, "hcp_plan_varlen_tiles")
+        self.num_tiles = rc
+        self.entries_dev = _to_device(arr, device)
+        self.tiles_dev = _to_device(tiles, device)
+        self.device = device
+
+    def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
+            num_kv_heads: int, scale: float) -> None:
+        if self.num_tiles == 0:
+            return
+        num_heads, head_dim = q.shape[1], q.shape[2]
+        L = _lib.lib()
+        with torch.cuda.device(q.device):
+            rc = L.hcp_attn_fwd_varlen(
+                q.data_ptr(), q.stride(0), q.stride(1),
+                out.data_ptr(), out.stride(0), out.stride(1),
+                lse.data_ptr(), lse.stride(0),
+                self.entries_dev.data_ptr(), self.num_entries,
+                self.tiles_dev.data_ptr(), self.num_tiles,
+                num_heads, num_kv_heads, head_dim, float(scale),
+                int(self.causal), int(self.paged), _lib.dtype_code(q.dtype),
+                _lib.stream_ptr(q.device),
+            )
+        _lib.check(rc, "hcp_attn_fwd_varlen")
+
+
+def varlen_attn_with_lse(
+    q: torch.Tensor,
+    entries: list[VarlenEntry],
+    causal: bool,
+    num_kv_heads: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """One launch over all entries.  Rows not covered by an entry are left as
+    given (``out``/``lse`` allocated here start as 0 / -inf)."""
+    if q.dtype not in (torch.float16, torch.bfloat16) or q.stride(-1) != 1:
+        raise ValueError("q must be float16/bfloat16 with contiguous head_dim")
+    paged = bool(entries) and entries[0].kv.block_table != 0
+    if out is None:
+        out = torch.zeros_like(q, memory_format=torch.contiguous_format)
+    if lse is None:
+        lse = torch.full((q.shape[1], q.shape[0]), float("-inf"), dtype=torch.float32,
+                         device=q.device)
+    VarlenLaunch(entries, causal, paged, q.device).run(q, out, lse, num_kv_heads, scale)
+    return out, lse
+
+
+def choose_split_tokens(seg_lens: list[int], num_kv_heads: int,
+                        target_workgroups: int = 2048, minimum: int = 256,
+                        maximum: int = 8192) -> int:
+    """Split size from the batch's total key count.
+
+    Aims at ``target_workgroups`` (split, KV head) workgroups -- 8 per CU on
+    256 CUs -- so every CU streams K/V with several waves in flight, while
+    each split stays long enough that its fp32 partial is small next to the
+    K/V it summarises.  Rounded to 64 keys.
+    """
+    total = sum(seg_lens) * num_kv_heads
+    if total == 0:
+        return minimum
+    s = -(-total // target_workgroups)
+    s = ((s + 63) // 64) * 64
+    return max(minimum, min(maximum, s))
+
+
+class DecodeBatch:
+    """A planned split-KV decode: entries, splits and workspace on the device.
+
+    ``segments[s]`` lists the KV segments of sequence ``s`` (all keys visible
+    to its single query, e.g. the staged peer prefix and the local paged KV
+    including the current token).
+    """
+
+    def __init__(self, segments: list[list[KvSegment]], num_heads: int, num_kv_heads: int,
+                 head_dim: int, device: torch.device, split_tokens: int | None = None):
+        L = _lib.lib()
+        entries, seq_of = [], []
+        for s, segs in enumerate(segments):
+            for seg in segs:
+                entries.append(make_entry(s, 1, seg, 0))
+                seq_of.append(s)
+        self.num_seqs = len(segments)
+        self.num_entries = len(entries)
+        if split_tokens is None:
+            split_tokens = choose_split_tokens([e.kv.len for e in entries], num_kv_heads)
+        self.split_tokens = split_tokens
+        arr = (VarlenEntry * max(self.num_entries, 1))(*entries)
+        seq_arr = (ctypes.c_int32 * max(self.num_entries, 1))(*seq_of)
+        cap = sum(-(-e.kv.len // split_tokens) for e in entries)
+        splits = (DecodeSplit * max(cap, 1))()
+        starts = (ctypes.c_int32 * (self.num_seqs + 1))()
+        rc = L.hcp_plan_decode_splits(ctypes.addressof(arr), self.num_entries,
+                                      ctypes.addressof(seq_arr), self.num_seqs, 0,
+                                      split_tokens, ctypes.addressof(splits), cap,
+                                      ctypes.addressof(starts))
+        _lib.check(rc, "hcp_plan_decode_splits")
+        self.num_splits = rc
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.entries_dev = _to_device(arr, device)
+        self.splits_dev = _to_device(splits, device)
+        self.starts_dev = _to_device(starts, device)
+        self.ws_bytes = int(L.hcp_decode_workspace_bytes(max(rc, 1), num_heads, head_dim))
+        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+
+    def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
+            scale: float) -> None:
+        L = _lib.lib()
+        with torch.cuda.device(q.device):
+            rc = L.hcp_decode_splitkv(
+                q.data_ptr(), q.stride(0), q.stride(1),
+                self.entries_dev.data_ptr(), self.num_entries,
+                self.splits_dev.data_ptr(), self.num_splits,
+                self.starts_dev.data_ptr(), self.num_seqs,
+                self.workspace.data_ptr(), self.ws_bytes,
+                out.data_ptr(), out.stride(0), out.stride(1),
+                lse.data_ptr() if lse is not None else None,
+                lse.stride(0) if lse is not None else 0,
+                self.num_heads, self.num_kv_heads, self.head_dim, float(scale),
+                _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
+            )
+        _lib.check(rc, "hcp_decode_splitkv")
+
+
+def decode_attn(
+    q: torch.Tensor,
+    segments: list[list[KvSegment]],
+    num_kv_heads: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+    with_lse: bool = False,
+    split_tokens: int | None = None,
+):
+    """Split-KV decode: q ``[S, H, D]`` (one token per sequence) over all
+    segments of each sequence, merged.  Returns out (and lse ``[H, S]``)."""
+    if q.dtype not in (torch.float16, torch.bfloat16) or q.stride(-1) != 1:
+        raise ValueError("q must be float16/bfloat16 with contiguous head_dim")
+    if len(segments) != q.shape[0]:
+        raise ValueError("one segment list per query row")
+    s, h, d = q.shape
+    batch = DecodeBatch(segments, h, num_kv_heads, d, q.device, split_tokens)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((h, s), dtype=torch.float32, device=q.device) if with_lse else None
+    batch.run(q, out, lse, scale)
+    return (out, lse) if with_lse else out

@@ -1,0 +1,84 @@
+"""GPU parity: split-KV decode (hcp_decode_splitkv) against the oracle.
+
+Each sequence has one query token, a contiguous peer segment and a paged
+local segment (all keys visible, ring_backend.py:663-679 / :820-830 with
+tq == 1); the reference result is local attention and peer attention merged
+(ring_backend.py:831, ring_decode.py:46-61).
+"""
+
+import pytest
+import torch
+
+from hcp_vllm_plugin_amd.varlen import PagedCache, decode_attn, segment_contiguous, segment_paged
+from oracle import ring_oracle as orc
+from tests._util import LSE_TOL, OUT_TOL, max_err, randn, scale_for
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(dev, h, hkv, d, dtype, peer_lens, loc_lens, bs, seed, split):
+    gen = torch.Generator().manual_seed(seed)
+    s = len(peer_lens)
+    blocks = [-(-l // bs) for l in loc_lens]
+    nb = sum(blocks) + 2
+    cache = randn(gen, (nb, hkv, bs, 2 * d), dtype)
+    perm = torch.randperm(nb, generator=gen).to(torch.int32)
+    bt = torch.zeros(s, max(max(blocks), 1), dtype=torch.int32)
+    o = 0
+    for r, n in enumerate(blocks):
+        bt[r, :n] = perm[o:o + n]
+        o += n
+    q = randn(gen, (s, h, d), dtype)
+    pk = randn(gen, (sum(peer_lens), hkv, d), dtype)
+    pv = randn(gen, (sum(peer_lens), hkv, d), dtype)
+    cd, btd, qd, pkd, pvd = cache.to(dev), bt.to(dev), q.to(dev), pk.to(dev), pv.to(dev)
+    pc = PagedCache.from_tensor(cd)
+    segs, ps = [], 0
+    for r in range(s):
+        segs.append([segment_contiguous(pkd, pvd, ps, peer_lens[r]),
+                     segment_paged(pc, btd[r], 0, loc_lens[r])])
+        ps += peer_lens[r]
+    scale = scale_for(d)
+    out, lse = decode_attn(qd, segs, hkv, scale, with_lse=True, split_tokens=split)
+    torch.cuda.synchronize()
+    ps = 0
+    for r in range(s):
+        kl, vl = orc.gather_paged(cache.float(), bt[r], 0, loc_lens[r], "v031")
+        qr = q[r:r + 1].float()
+        ro_l, rl_l = orc.attn_with_lse(qr, kl, vl, scale, loc_lens[r] - 1)
+        ro_p, rl_p = orc.attn_with_lse(qr, pk[ps:ps + peer_lens[r]].float(),
+                                       pv[ps:ps + peer_lens[r]].float(), scale, None)
+        ro, rl = orc.merge_pair(ro_l, rl_l, ro_p, rl_p)
+        assert max_err(out[r:r + 1], ro) <= OUT_TOL[dtype], (r, max_err(out[r:r + 1], ro))
+        assert max_err(lse[:, r:r + 1], rl) <= LSE_TOL, r
+        ps += peer_lens[r]
+
+
+@pytest.mark.parametrize("split", [None, 64, 256, 1000])
+def test_decode_qwen7b_shape(dev, split):
+    _case(dev, 28, 4, 128, torch.bfloat16,
+          peer_lens=[4096, 0, 1000, 33, 2048, 7],
+          loc_lens=[512, 700, 1, 2048, 33, 1500], bs=16, seed=51, split=split)
+
+
+def test_decode_llama70b_shape(dev):
+    _case(dev, 64, 8, 128, torch.bfloat16, peer_lens=[3000, 100], loc_lens=[900, 17],
+          bs=16, seed=52, split=None)
+
+
+def test_decode_fp16_d64(dev):
+    _case(dev, 14, 2, 64, torch.float16, peer_lens=[512, 2048, 0], loc_lens=[100, 1, 600],
+          bs=16, seed=53, split=128)
+
+
+def test_decode_empty_sequence(dev):
+    """A sequence whose segments are all empty gets out 0, lse -inf."""
+    h, hkv, d = 28, 4, 128
+    q = torch.randn(2, h, d, device=dev).to(torch.bfloat16)
+    k = torch.randn(100, hkv, d, device=dev).to(torch.bfloat16)
+    segs = [[segment_contiguous(k, k, 0, 100)], [segment_contiguous(k, k, 0, 0)]]
+    out, lse = decode_attn(q, segs, hkv, 0.088, with_lse=True)
+    torch.cuda.synchronize()
+    assert torch.all(out[1] == 0) and torch.all(torch.isneginf(lse[:, 1]))
+    ro, rl = orc.attn_with_lse(q[:1].float().cpu(), k.float().cpu(), k.float().cpu(), 0.088, None)
+    assert max_err(out[:1], ro) <= OUT_TOL[torch.bfloat16]

@@ -1,0 +1,110 @@
+"""GPU parity: batched varlen prefill (hcp_attn_fwd_varlen) with the local
+segment read in place from the paged cache, the peer segment from packed
+contiguous KV, and one merge -- against the oracle's per-request
+gather + attention + merge (ring_backend.py:611-832).
+"""
+
+import pytest
+import torch
+
+from hcp_vllm_plugin_amd import merge_attn_states
+from hcp_vllm_plugin_amd.varlen import (
+    PagedCache,
+    make_entry,
+    segment_contiguous,
+    segment_paged,
+    varlen_attn_with_lse,
+)
+from oracle import ring_oracle as orc
+from tests._util import LSE_TOL, OUT_TOL, max_err, randn, scale_for
+
+pytestmark = pytest.mark.gpu
+
+
+def _build(dev, layout, lens, peers, h, hkv, d, dtype, bs, seed):
+    gen = torch.Generator().manual_seed(seed)
+    blocks_per = [-(-(p + l) // bs) for p, l in zip(peers, lens)]
+    nb = sum(blocks_per) + 3
+    if layout == "v031":
+        cache = randn(gen, (nb, hkv, bs, 2 * d), dtype)
+    else:
+        cache = randn(gen, (nb, 2, bs, hkv, d), dtype)
+    perm = torch.randperm(nb, generator=gen).to(torch.int32)
+    maxb = max(blocks_per)
+    bt = torch.zeros(len(lens), maxb, dtype=torch.int32)
+    o = 0
+    for r, nbk in enumerate(blocks_per):
+        bt[r, :nbk] = perm[o:o + nbk]
+        o += nbk
+    q = randn(gen, (sum(lens), h, d), dtype)
+    peer = randn(gen, (sum(peers), 2, hkv, d), dtype)
+    return cache, bt, q, peer
+
+
+@pytest.mark.parametrize("layout", ["v031", "v023"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_varlen_local_paged_peer_contiguous(dev, layout, dtype):
+    h, hkv, d, bs = 28, 4, 128, 16
+    lens = [300, 1, 129, 700, 64, 0, 257]
+    peers = [512, 48, 1024, 0, 16, 32, 400]
+    cache, bt, q, peer = _build(dev, layout, lens, peers, h, hkv, d, dtype, bs, seed=41)
+    cd, btd, qd, pd = cache.to(dev), bt.to(dev), q.to(dev), peer.to(dev)
+    pc = PagedCache.from_tensor(cd)
+    pk, pv = pd[:, 0], pd[:, 1]
+    loc_e, peer_e = [], []
+    qs, ps = 0, 0
+    for r, (L, P) in enumerate(zip(lens, peers)):
+        loc_e.append(make_entry(qs, L, segment_paged(pc, btd[r], P, L), 0))
+        peer_e.append(make_entry(qs, L, segment_contiguous(pk, pv, ps, P), 0))
+        qs += L
+        ps += P
+    scale = scale_for(d)
+    o_loc, lse_loc = varlen_attn_with_lse(qd, loc_e, True, hkv, scale)
+    o_peer, lse_peer = varlen_attn_with_lse(qd, peer_e, False, hkv, scale)
+    out = torch.empty_like(o_loc)
+    merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc)
+    torch.cuda.synchronize()
+    qs, ps = 0, 0
+    for r, (L, P) in enumerate(zip(lens, peers)):
+        qr = q[qs:qs + L].float()
+        kl, vl = orc.gather_paged(cache.float(), bt[r], P, L, layout)
+        rl, rll = orc.attn_with_lse(qr, kl, vl, scale, 0)
+        rp, rpl = orc.attn_with_lse(qr, peer[ps:ps + P, 0].float(), peer[ps:ps + P, 1].float(),
+                                    scale, None)
+        rm = orc.lse_merge(rl, rll, rp, rpl)
+        sl = slice(qs, qs + L)
+        assert max_err(o_loc[sl], rl) <= OUT_TOL[dtype], r
+        assert max_err(lse_loc[:, sl], rll) <= LSE_TOL, r
+        assert max_err(o_peer[sl], rp) <= OUT_TOL[dtype], r
+        assert max_err(lse_peer[:, sl], rpl) <= LSE_TOL, r
+        assert max_err(out[sl], rm) <= OUT_TOL[dtype], r
+        qs += L
+        ps += P
+
+
+def test_varlen_offsets_and_unaligned_starts(dev):
+    """Causal offsets != 0 and paged segments starting mid-block."""
+    h, hkv, d, bs = 8, 2, 128, 16
+    lens = [100, 37, 200]
+    peers = [5, 0, 77]   # local segment starts at token P (not block aligned)
+    offs = [0, 20, 130]
+    cache, bt, q, _ = _build(dev, "v031", lens, peers, h, hkv, d, torch.bfloat16, bs, seed=42)
+    cd, btd, qd = cache.to(dev), bt.to(dev), q.to(dev)
+    pc = PagedCache.from_tensor(cd)
+    ent, qs = [], 0
+    kv_lens = [L + o for L, o in zip(lens, offs)]  # keys visible up to offset+row
+    # widen the cache view: segment length may exceed q rows when offset > 0
+    for r, (L, P, o) in enumerate(zip(lens, peers, offs)):
+        kl = min(kv_lens[r], bt.shape[1] * bs - P)
+        ent.append(make_entry(qs, L, segment_paged(pc, btd[r], P, kl), o))
+        qs += L
+    o_, lse_ = varlen_attn_with_lse(qd, ent, True, hkv, scale_for(d))
+    torch.cuda.synchronize()
+    qs = 0
+    for r, (L, P, o) in enumerate(zip(lens, peers, offs)):
+        e = ent[r]
+        kl, vl = orc.gather_paged(cache.float(), bt[r], P, e.kv.len, "v031")
+        ro, rl = orc.attn_with_lse(q[qs:qs + L].float(), kl, vl, scale_for(d), o)
+        assert max_err(o_[qs:qs + L], ro) <= OUT_TOL[torch.bfloat16]
+        assert max_err(lse_[:, qs:qs + L], rl) <= LSE_TOL
+        qs += L
