@@ -15,32 +15,58 @@
 //    operand read from LDS, Q^T the B operand held in registers for the whole
 //    kernel.  In the 32x32 accumulator layout a lane owns one column, so each
 //    lane owns ONE query row and 16 of its keys per 32-key block: the row max
-//    is an in-register max plus one exchange with lane ^ 32, and the row sum
-//    stays a per-lane partial until the epilogue.
+//    is an in-register max3 tree plus one exchange with lane ^ 32, and the
+//    row sum stays a per-lane partial until the epilogue.
 //  * O^T = V^T P^T on the same MFMA: P^T comes straight from the S^T
-//    registers (the key order inside the k dimension is a free permutation,
-//    matched by the layout V^T is stored in), V^T is the A operand from LDS.
-//  * K (64 keys x D) and V^T (D x 64 keys) tiles are double-buffered in LDS:
-//    the global loads of tile n+1 are issued before the MFMAs of tile n and
-//    written to the other buffer after them; one barrier per tile.  V is
-//    transposed on its way into LDS (each thread owns a 4-d x 8-key or
-//    4-d x 4-key sub-block).  Both tiles use an XOR swizzle of 16-byte slots
-//    so the MFMA operand reads and the tile writes are bank-conflict free.
-//  * Causal tiles above the diagonal of a wave are skipped; masking is only
-//    applied on diagonal and ragged tiles.
+//    registers (the key order inside the k dimension is a free permutation);
+//    the V^T A operand is read from a row-major V tile with the gfx950
+//    transposing LDS read ds_read_b64_tr_b16: inside each 16-lane block,
+//    lane 4e+a reads 4 consecutive d of key kbase+e and every lane receives 4
+//    keys of one d column.
+//  * K and V tiles (64 keys x D, row-major, 16-byte slots XOR-swizzled by
+//    2*(row&3) | (row>>2 & 1) so both the K reads and the transposing V reads
+//    are bank-conflict free) are filled by global_load_lds_dwordx4: HBM/L2 ->
+//    LDS with no register staging and no VALU work.  Two tile buffers are
+//    separate __shared__ objects and the key loop is unrolled by two, so the
+//    loads for tile n+1 stay in flight while tile n is computed (one barrier
+//    per tile).
+//  * Lazy rescale: the running max used as the exponent reference is only
+//    raised when some row's tile max exceeds it by more than 2^8; otherwise P
+//    values are bounded by 256 and the O rescale (64 multiplies per lane) is
+//    skipped.  The result is exact: O, l and lse all use the same reference.
+//  * Causal tiles above a wave's diagonal are skipped; masking runs only on
+//    diagonal and ragged tiles.  Ragged tiles clamp key rows into the segment
+//    (the clamped rows are masked in S, and their finite V values meet P = 0),
+//    so no load goes out of bounds and no load is predicated.
 //  * The local (paged) segment is read in place through the block table
 //    (hcp_kv_segment), replacing the per-request gather copy of
-//    ring_backend.py:617-624.
+//    ring_backend.py:617-624; block ids are fetched two tiles ahead.
 #include "params.h"
 
 namespace hcp {
 
+constexpr float kRescaleThresh = 8.0f;  // log2 units: P <= 2^8 between rescales
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+#define HCP_LDS(T) __attribute__((address_space(3))) T
 
-__device__ __forceinline__ int swap_bits23(int x) {
-  return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1);
+__device__ __forceinline__ int tile_swz(int row) { return (2 * (row & 3)) | ((row >> 2) & 1); }
+
+__device__ __forceinline__ void lds_load16(const char* g, HCP_LDS(char)* l) {
+  __builtin_amdgcn_global_load_lds(
+      reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(g)),
+      reinterpret_cast<HCP_LDS(void)*>(l), 16, 0, 0);
 }
-__device__ __forceinline__ int vt_swz(int d) { return (d + (d >> 3)) & 7; }
+
+template <typename V8>
+__device__ __forceinline__ V8 lds_read16(const HCP_LDS(char)* p) {
+  return __builtin_bit_cast(V8, *reinterpret_cast<const HCP_LDS(u32x4)*>(p));
+}
+
+__device__ __forceinline__ i16x4 lds_read_tr(const HCP_LDS(char)* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<HCP_LDS(i16x4)*>(const_cast<HCP_LDS(char)*>(p)));
+}
 
 template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
@@ -49,16 +75,15 @@ fa_fwd_kernel(FwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::vec8;
   constexpr int BM = kFwdBM, BN = kFwdBN;
-  constexpr int KSTEPS = D / 16;     // QK^T k-steps of 16
-  constexpr int DBLK = D / 32;       // 32-row blocks of O^T
-  constexpr int KSLOTS = D / 8;      // 16-byte slots per K row
-  constexpr int KROWS_PER_PASS = kFwdThreads / KSLOTS;
-  constexpr int KLOADS = BN / KROWS_PER_PASS;  // 16-byte K loads per thread
-  constexpr int VK = D / 16;         // keys per thread in the V^T transpose
-  constexpr int DQ = D / 4;          // 4-wide d quads
+  constexpr int ROWB = D * 2;                  // bytes per tile row
+  constexpr int TILEB = BN * ROWB;             // bytes per K (or V) tile
+  constexpr int NI = TILEB / (kFwdThreads * 16);  // direct loads per thread per tile
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBLK = D / 32;
   static_assert(D == 64 || D == 128, "head_dim");
 
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][BN * D + D * BN];
+  __shared__ __attribute__((aligned(1024))) char bufA[2 * TILEB];  // K | V
+  __shared__ __attribute__((aligned(1024))) char bufB[2 * TILEB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,15 +108,11 @@ fa_fwd_kernel(FwdParams p) {
     e = p.entries[ent];
   } else {
     e = p.single;
-    // heaviest (last) query block first for causal
-    qb = CAUSAL ? (p.num_tiles - 1 - tile) : tile;
+    qb = CAUSAL ? (p.num_tiles - 1 - tile) : tile;  // heaviest first
   }
   const int64_t q_len = e.q_len;
-  const int64_t kv_len = e.kv.len;
+  const int kv_len = static_cast<int>(e.kv.len);
   const int64_t off = e.causal_offset;
-
-  KvAddr kva;
-  kva.init(e.kv);
 
   // ---- Q^T fragments (B operand): lane owns query row r32 ----
   const int64_t qi = static_cast<int64_t>(qb) * BM + wave * 32 + r32;
@@ -100,8 +121,7 @@ fa_fwd_kernel(FwdParams p) {
   {
     const char* qrow = reinterpret_cast<const char*>(p.q) +
                        ((e.q_start + (q_valid ? qi : 0)) * p.q_stride_tok +
-                        static_cast<int64_t>(head) * p.q_stride_head) *
-                           2;
+                        static_cast<int64_t>(head) * p.q_stride_head) * 2;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
       u32x4 x = q_valid ? ldg16(qrow + (16 * s + 8 * g) * 2) : u32x4{0, 0, 0, 0};
@@ -112,171 +132,211 @@ fa_fwd_kernel(FwdParams p) {
   // ---- key range of the workgroup and of this wave ----
   int64_t n_end = kv_len;
   if (CAUSAL) {
-    int64_t lim = off + static_cast<int64_t>(qb) * BM + BM;
+    const int64_t lim = off + static_cast<int64_t>(qb) * BM + BM;
     n_end = n_end < lim ? n_end : lim;
   }
   if (n_end < 0) n_end = 0;
   const int ntiles = static_cast<int>((n_end + BN - 1) / BN);
   const int64_t wave_q0 = static_cast<int64_t>(qb) * BM + wave * 32;
-  const int64_t wave_last = CAUSAL ? off + wave_q0 + 31 : kv_len - 1;
+  const int64_t wave_last = CAUSAL ? off + wave_q0 + 31 : static_cast<int64_t>(kv_len) - 1;
 
-  // ---- tile loader (global -> registers -> LDS) ----
-  const int kc = tid % KSLOTS;      // 16-byte chunk of a K row
-  const int kr0 = tid / KSLOTS;     // first K row of this thread
-  const int vdq = tid % DQ;         // d quad for V
-  const int vpg = tid / DQ;         // V^T position group (VK positions)
-  u32x4 kreg[KLOADS];
-  u32x2 vreg[VK];
+  // ---- direct tile loads: lane's row / chunk for load instruction i ----
+  // instruction i of wave w fills LDS bytes [(w*NI+i)*1024, +1024)
+  int lrow[NI];
+  int lchunk[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int o = (wave * NI + i) * 1024 + lane * 16;
+    lrow[i] = o / ROWB;
+    lchunk[i] = ((o % ROWB) / 16) ^ tile_swz(lrow[i]);
+  }
+  const int64_t rowb_g = e.kv.stride_tok * 2;  // bytes between tokens in HBM
+  const char* kseg;
+  const char* vseg;
+  int bs_shift = 0, bs_mask = 0;
+  const int32_t* bt = reinterpret_cast<const int32_t*>(e.kv.block_table);
+  int64_t blockb = 0;
+  if constexpr (PAGED) {
+    kseg = reinterpret_cast<const char*>(e.kv.k_addr) + static_cast<int64_t>(kvh) * e.kv.stride_head * 2;
+    vseg = reinterpret_cast<const char*>(e.kv.v_addr) + static_cast<int64_t>(kvh) * e.kv.stride_head * 2;
+    bs_shift = 31 - __builtin_clz(e.kv.block_size);
+    bs_mask = e.kv.block_size - 1;
+    blockb = e.kv.stride_block * 2;
+  } else {
+    const int64_t base = (e.kv.start * e.kv.stride_tok + static_cast<int64_t>(kvh) * e.kv.stride_head) * 2;
+    kseg = reinterpret_cast<const char*>(e.kv.k_addr) + base;
+    vseg = reinterpret_cast<const char*>(e.kv.v_addr) + base;
+  }
+  // paged: block ids of the lane's rows for the next tile to be issued
+  int bnext[NI];
 
-  auto load_tile = [&](int64_t n0) {
+  auto fetch_blocks = [&](int tile_idx) {
+    if constexpr (PAGED) {
 #pragma unroll
-    for (int rr = 0; rr < KLOADS; ++rr) {
-      const int64_t key = n0 + kr0 + rr * KROWS_PER_PASS;
-      if (key < kv_len) {
-        const int64_t o = kva.offset<PAGED>(key, kvh) + kc * 8;
-        kreg[rr] = ldg16(kva.k + o * 2);
-      } else {
-        kreg[rr] = u32x4{0, 0, 0, 0};
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < VK; ++j) {
-      const int64_t key = n0 + swap_bits23(VK * vpg + j);
-      if (key < kv_len) {
-        const int64_t o = kva.offset<PAGED>(key, kvh) + vdq * 4;
-        vreg[j] = ldg8(kva.v + o * 2);
-      } else {
-        vreg[j] = u32x2{0, 0};
+      for (int i = 0; i < NI; ++i) {
+        int key = tile_idx * BN + lrow[i];
+        key = key < kv_len ? key : kv_len - 1;
+        bnext[i] = bt[(e.kv.start + key) >> bs_shift];
       }
     }
   };
 
-  auto store_tile = [&](int buf) {
-    uint16_t* Ks = smem[buf];
-    uint16_t* Vt = smem[buf] + BN * D;
+  auto issue_tile = [&](int tile_idx, HCP_LDS(char)* dst) {
+    const int n0 = tile_idx * BN;
+    const bool ragged = n0 + BN > kv_len;
 #pragma unroll
-    for (int rr = 0; rr < KLOADS; ++rr) {
-      const int row = kr0 + rr * KROWS_PER_PASS;
-      const int slot = row * KSLOTS + (kc ^ (row & 7));
-      *reinterpret_cast<u32x4*>(Ks + slot * 8) = kreg[rr];
-    }
-#pragma unroll
-    for (int dd = 0; dd < 4; ++dd) {
-      const int d = 4 * vdq + dd;
-      const int word = dd >> 1;
-      uint32_t packed[VK / 2];
-#pragma unroll
-      for (int j = 0; j < VK / 2; ++j) {
-        uint32_t a = vreg[2 * j][word], b = vreg[2 * j + 1][word];
-        packed[j] = (dd & 1) ? ((a >> 16) | (b & 0xffff0000u))
-                             : ((a & 0xffffu) | (b << 16));
-      }
-      if constexpr (VK == 8) {
-        const int slot = vpg ^ vt_swz(d);
-        *reinterpret_cast<u32x4*>(Vt + d * BN + slot * 8) =
-            u32x4{packed[0], packed[1], packed[2], packed[3]};
+    for (int i = 0; i < NI; ++i) {
+      int key = n0 + lrow[i];
+      if (ragged) key = key < kv_len ? key : kv_len - 1;
+      int64_t go;
+      if constexpr (PAGED) {
+        const int64_t x = e.kv.start + key;
+        go = static_cast<int64_t>(bnext[i]) * blockb + (x & bs_mask) * rowb_g + lchunk[i] * 16;
       } else {
-        const int slot = (vpg >> 1) ^ vt_swz(d);
-        *reinterpret_cast<u32x2*>(Vt + d * BN + slot * 8 + (vpg & 1) * 4) =
-            u32x2{packed[0], packed[1]};
+        go = static_cast<int64_t>(key) * rowb_g + lchunk[i] * 16;
       }
+      HCP_LDS(char)* l = dst + (wave * NI + i) * 1024;
+      lds_load16(kseg + go, l);
+      lds_load16(vseg + go, l + TILEB);
     }
   };
+
+  // ---- LDS read addresses (loop invariant, per lane) ----
+  // K (A operand of S^T): row 32*blk + r32, 16-byte chunk 2s+g
+  const int kx = tile_swz(r32);
+  int koff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) koff[s] = r32 * ROWB + (((2 * s + g) ^ kx) * 16);
+  // V (transposing read): block beta = lane/16, i = lane%16 = 4*ee + aa
+  const int beta = lane >> 4, ee = (lane & 15) >> 2, aa = lane & 3;
+  const int vg = beta >> 1;
+  const int vx = (2 * ee) | vg;
+  const int vs0 = 2 * (beta & 1) + (aa >> 1);
+  int voff[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+    voff[par] = (4 * vg + ee) * ROWB + (((4 * par + vs0) ^ vx) * 16) + (aa & 1) * 8;
 
   // ---- online softmax state ----
   const float c = p.scale_log2;
-  float m_run = -INFINITY;
+  float m_ref = -INFINITY;
   float l_run = 0.f;
   f32x16 oacc[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) oacc[i] = f32x16{};
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int64_t n0 = static_cast<int64_t>(it) * BN;
-    const bool more = it + 1 < ntiles;
-    if (more) load_tile(n0 + BN);
-    const uint16_t* Ks = smem[it & 1];
-    const uint16_t* Vt = smem[it & 1] + BN * D;
-
-    if (!CAUSAL || n0 <= wave_last) {
-      // S^T = K Q^T : two 32-key blocks
-      f32x16 s0 = f32x16{}, s1 = f32x16{};
+  auto compute_tile = [&](const HCP_LDS(char)* Ks, int n0) {
+    if (CAUSAL && n0 > wave_last) return;  // whole tile above this wave's diagonal
+    const HCP_LDS(char)* Vs = Ks + TILEB;
+    // S^T = K Q^T
+    f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const int sl = 2 * s + g;
-        const int row0 = r32, row1 = 32 + r32;
-        V8 k0 = as_vec8<V8>(*reinterpret_cast<const u32x4*>(
-            Ks + (row0 * KSLOTS + (sl ^ (row0 & 7))) * 8));
-        V8 k1 = as_vec8<V8>(*reinterpret_cast<const u32x4*>(
-            Ks + (row1 * KSLOTS + (sl ^ (row1 & 7))) * 8));
-        s0 = E::mfma32(k0, qf[s], s0);
-        s1 = E::mfma32(k1, qf[s], s1);
-      }
-      // masking on ragged / diagonal tiles
-      const bool ragged = n0 + BN > kv_len;
-      const bool diag = CAUSAL && (n0 + BN - 1 > off + wave_q0);
-      if (ragged || diag) {
-        const int64_t lim = CAUSAL ? off + qi : kv_len - 1;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-          const int64_t key0 = n0 + kk, key1 = n0 + 32 + kk;
-          if (key0 >= kv_len || key0 > lim) s0[r] = -INFINITY;
-          if (key1 >= kv_len || key1 > lim) s1[r] = -INFINITY;
-        }
-      }
-      float mx = s0[0];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx * c);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      float rs = 0.f;
+    for (int s = 0; s < KSTEPS; ++s) {
+      const int o = koff[s & 3] + (s >> 2) * 128;
+      const V8 k0 = lds_read16<V8>(Ks + o);
+      const V8 k1 = lds_read16<V8>(Ks + o + 32 * ROWB);
+      s0 = E::mfma32(k0, qf[s], s0);
+      s1 = E::mfma32(k1, qf[s], s1);
+    }
+    // masking on ragged / diagonal tiles (wave-uniform branch)
+    const bool ragged = n0 + BN > kv_len;
+    const bool diag = CAUSAL && (n0 + BN - 1 > off + wave_q0);
+    if (ragged || diag) {
+      const int lim_r = kv_len - 1 - n0;
+      const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
+      const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
+      const int lim = lim_r < lim_c ? lim_r : lim_c;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s0[r] = fast_exp2(__builtin_fmaf(s0[r], c, -m_use));
-        s1[r] = fast_exp2(__builtin_fmaf(s1[r], c, -m_use));
-        rs += s0[r] + s1[r];
-      }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
-
-      // P^T fragments: step t uses S^T block t/2, registers 8(t%2)..+7
-      V8 pf[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const f32x16& sb = (t < 2) ? s0 : s1;
-        const int base = 8 * (t & 1);
-        u32x4 w;
-        w[0] = pack2<T>(sb[base + 0], sb[base + 1]);
-        w[1] = pack2<T>(sb[base + 2], sb[base + 3]);
-        w[2] = pack2<T>(sb[base + 4], sb[base + 5]);
-        w[3] = pack2<T>(sb[base + 6], sb[base + 7]);
-        pf[t] = as_vec8<V8>(w);
-      }
-      // O^T += V^T P^T
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) {
-        const int d = 32 * db + r32;
-        const int sw = vt_swz(d);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          V8 vf = as_vec8<V8>(*reinterpret_cast<const u32x4*>(
-              Vt + d * BN + ((2 * t + g) ^ sw) * 8));
-          oacc[db] = E::mfma32(vf, pf[t], oacc[db]);
-        }
+        const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
+        if (kk > lim) s0[r] = -INFINITY;
+        if (kk + 32 > lim) s1[r] = -INFINITY;
       }
     }
-    if (more) store_tile((it + 1) & 1);
+    // row max: max3 tree over 32 values, then the other half of the row
+    float m4[4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int b = 4 * q4;
+      float a = __builtin_fmaxf(__builtin_fmaxf(s0[b], s0[b + 1]), s0[b + 2]);
+      a = __builtin_fmaxf(__builtin_fmaxf(a, s0[b + 3]), s1[b]);
+      a = __builtin_fmaxf(__builtin_fmaxf(a, s1[b + 1]), s1[b + 2]);
+      m4[q4] = __builtin_fmaxf(a, s1[b + 3]);
+    }
+    float mx = __builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3]));
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+    const float mxs = mx * c;
+    if (__any(mxs > m_ref + kRescaleThresh)) {
+      const float m_new = __builtin_fmaxf(m_ref, mxs);
+      const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
+      m_ref = m_new;
+    }
+    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+    float rs = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = fast_exp2(__builtin_fmaf(s0[r], c, -m_use));
+      s1[r] = fast_exp2(__builtin_fmaf(s1[r], c, -m_use));
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) rs += (s0[r] + s0[r + 1]) + (s1[r] + s1[r + 1]);
+    l_run += rs;
+    // P^T fragments: step t uses S^T block t/2, registers 8(t%2)..+7
+    V8 pf[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f32x16& sb = (t < 2) ? s0 : s1;
+      const int b = 8 * (t & 1);
+      u32x4 w;
+      w[0] = pack2<T>(sb[b + 0], sb[b + 1]);
+      w[1] = pack2<T>(sb[b + 2], sb[b + 3]);
+      w[2] = pack2<T>(sb[b + 4], sb[b + 5]);
+      w[3] = pack2<T>(sb[b + 6], sb[b + 7]);
+      pf[t] = as_vec8<V8>(w);
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db) {
+      const int vb = voff[db & 1] + (db >> 1) * 128;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const i16x4 lo = lds_read_tr(Vs + vb + (16 * t) * ROWB);
+        const i16x4 hi = lds_read_tr(Vs + vb + (16 * t + 8) * ROWB);
+        u32x4 w;
+        w[0] = __builtin_bit_cast(u32x2, lo)[0];
+        w[1] = __builtin_bit_cast(u32x2, lo)[1];
+        w[2] = __builtin_bit_cast(u32x2, hi)[0];
+        w[3] = __builtin_bit_cast(u32x2, hi)[1];
+        oacc[db] = E::mfma32(as_vec8<V8>(w), pf[t], oacc[db]);
+      }
+    }
+  };
+
+  HCP_LDS(char)* A = (HCP_LDS(char)*)(bufA);
+  HCP_LDS(char)* B = (HCP_LDS(char)*)(bufB);
+
+  if (ntiles > 0) {
+    fetch_blocks(0);
+    issue_tile(0, A);
+    if (ntiles > 1) fetch_blocks(1);
+  }
+  __syncthreads();
+  for (int it = 0; it < ntiles; it += 2) {
+    if (it + 1 < ntiles) {
+      issue_tile(it + 1, B);
+      if (it + 2 < ntiles) fetch_blocks(it + 2);
+    }
+    compute_tile(A, it * BN);
+    __syncthreads();
+    if (it + 1 >= ntiles) break;
+    if (it + 2 < ntiles) {
+      issue_tile(it + 2, A);
+      if (it + 3 < ntiles) fetch_blocks(it + 3);
+    }
+    compute_tile(B, (it + 1) * BN);
     __syncthreads();
   }
 
@@ -300,7 +360,7 @@ fa_fwd_kernel(FwdParams p) {
     }
     if (g == 0) {
       p.lse[static_cast<int64_t>(head) * p.lse_stride_head + row] =
-          l_tot > 0.f ? m_run * kLn2 + __logf(l_tot) : -INFINITY;
+          l_tot > 0.f ? m_ref * kLn2 + __logf(l_tot) : -INFINITY;
     }
   }
 }

@@ -64,11 +64,21 @@ struct Elem<_Float16> {
   }
 };
 
-// Pack two floats into one dword of two 16-bit elements (lo = a, hi = b).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Pack two floats into one dword of two 16-bit elements (lo = a, hi = b),
+// round to nearest even: one v_cvt_pk_{bf16,f16}_f32 on gfx950.
 template <typename T>
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return static_cast<uint32_t>(Elem<T>::from_float(a)) |
-         (static_cast<uint32_t>(Elem<T>::from_float(b)) << 16);
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<__bf16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), f16x2));
 }
 
 template <typename V>
@@ -76,11 +86,15 @@ __device__ __forceinline__ V as_vec8(u32x4 x) {
   return __builtin_bit_cast(V, x);
 }
 
+typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+typedef const __attribute__((address_space(1))) u32x2 gu32x2;
+
+// Global-memory loads (global_load, not flat_load).
 __device__ __forceinline__ u32x4 ldg16(const void* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+  return *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p));
 }
 __device__ __forceinline__ u32x2 ldg8(const void* p) {
-  return *reinterpret_cast<const u32x2*>(p);
+  return *reinterpret_cast<gu32x2*>(reinterpret_cast<uintptr_t>(p));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) {
