@@ -114,6 +114,8 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, flo
   p.single.kv.len = tk;
   if (k_stride_tok != v_stride_tok || k_stride_head != v_stride_head)
     return fail(HCP_EUNSUPPORTED, "%s: k and v must share strides", who);
+  if (k_stride_tok <= 0 || k_stride_tok >= (int64_t{1} << 24))
+    return fail(HCP_EUNSUPPORTED, "%s: k token stride must be in (0, 2^24) elements", who);
   hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, false, false,
                                  static_cast<hipStream_t>(stream));
   return launch_status(e, who);

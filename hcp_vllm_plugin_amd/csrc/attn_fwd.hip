@@ -45,12 +45,26 @@
 
 namespace hcp {
 
+#ifndef HCP_MFMA_PRIO
+#define HCP_MFMA_PRIO 3
+#endif
+
 constexpr float kRescaleThresh = 8.0f;  // log2 units: P <= 2^8 between rescales
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define HCP_LDS(T) __attribute__((address_space(3))) T
 
-__device__ __forceinline__ int tile_swz(int row) { return (2 * (row & 3)) | ((row >> 2) & 1); }
+// XOR swizzle of the 16-byte slot index of tile row `row`.  gfx950 LDS has 64
+// banks of 4 bytes: a ds_read_b128 serves 16 lanes per cycle (16 consecutive
+// K rows, same logical slot -> the swizzle is a bijection on row & 15) and a
+// ds_read_b64_tr_b16 serves 32 lanes (4 key rows e = row & 3, 64 bytes each
+// -> rows e move to disjoint 64-byte slot groups).  For D = 64 two 128-byte
+// rows share the 256-byte bank space, so the row parity takes that role.
+template <int D>
+__device__ __forceinline__ int tile_swz(int row) {
+  if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
+  return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+}
 
 __device__ __forceinline__ void lds_load16(const char* g, HCP_LDS(char)* l) {
   __builtin_amdgcn_global_load_lds(
@@ -87,7 +101,7 @@ fa_fwd_kernel(FwdParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r32 = lane & 31;
   const int g = lane >> 5;
 
@@ -148,7 +162,7 @@ fa_fwd_kernel(FwdParams p) {
   for (int i = 0; i < NI; ++i) {
     const int o = (wave * NI + i) * 1024 + lane * 16;
     lrow[i] = o / ROWB;
-    lchunk[i] = ((o % ROWB) / 16) ^ tile_swz(lrow[i]);
+    lchunk[i] = ((o % ROWB) / 16) ^ tile_swz<D>(lrow[i]);
   }
   const int64_t rowb_g = e.kv.stride_tok * 2;  // bytes between tokens in HBM
   const char* kseg;
@@ -170,7 +184,7 @@ fa_fwd_kernel(FwdParams p) {
   // paged: block ids of the lane's rows for the next tile to be issued
   int bnext[NI];
 
-  auto fetch_blocks = [&](int tile_idx) {
+  auto fetch_blocks = [&](int tile_idx) __attribute__((always_inline)) {
     if constexpr (PAGED) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -181,41 +195,67 @@ fa_fwd_kernel(FwdParams p) {
     }
   };
 
-  auto issue_tile = [&](int tile_idx, HCP_LDS(char)* dst) {
+  // contiguous: per-lane 32-bit byte offsets inside a tile (loop invariant);
+  // the tile base is wave-uniform, so loads use the SGPR-base + VGPR-offset form
+  const uint32_t rowb32 = static_cast<uint32_t>(rowb_g);
+  uint32_t goff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) goff[i] = lrow[i] * rowb32 + lchunk[i] * 16u;
+
+  auto issue_tile = [&](int tile_idx, HCP_LDS(char)* dst) __attribute__((always_inline)) {
     const int n0 = tile_idx * BN;
     const bool ragged = n0 + BN > kv_len;
+    if constexpr (PAGED) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      int key = n0 + lrow[i];
-      if (ragged) key = key < kv_len ? key : kv_len - 1;
-      int64_t go;
-      if constexpr (PAGED) {
+      for (int i = 0; i < NI; ++i) {
+        int key = n0 + lrow[i];
+        if (ragged) key = key < kv_len ? key : kv_len - 1;
         const int64_t x = e.kv.start + key;
-        go = static_cast<int64_t>(bnext[i]) * blockb + (x & bs_mask) * rowb_g + lchunk[i] * 16;
-      } else {
-        go = static_cast<int64_t>(key) * rowb_g + lchunk[i] * 16;
+        const int64_t go =
+            static_cast<int64_t>(bnext[i]) * blockb + (x & bs_mask) * rowb_g + lchunk[i] * 16;
+        HCP_LDS(char)* l = dst + (wave * NI + i) * 1024;
+        lds_load16(kseg + go, l);
+        lds_load16(vseg + go, l + TILEB);
       }
-      HCP_LDS(char)* l = dst + (wave * NI + i) * 1024;
-      lds_load16(kseg + go, l);
-      lds_load16(vseg + go, l + TILEB);
+    } else {
+      const char* kt = kseg + static_cast<int64_t>(n0) * rowb_g;
+      const char* vt = vseg + static_cast<int64_t>(n0) * rowb_g;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        uint32_t o = goff[i];
+        if (ragged) {
+          const int key = n0 + lrow[i];
+          const int kc = key < kv_len ? key : kv_len - 1;
+          o = static_cast<uint32_t>(kc - n0) * rowb32 + lchunk[i] * 16u;
+        }
+        HCP_LDS(char)* l = dst + (wave * NI + i) * 1024;
+        lds_load16(kt + o, l);
+        lds_load16(vt + o, l + TILEB);
+      }
     }
   };
 
   // ---- LDS read addresses (loop invariant, per lane) ----
   // K (A operand of S^T): row 32*blk + r32, 16-byte chunk 2s+g
-  const int kx = tile_swz(r32);
-  int koff[4];
+  // (row + 32 has the same swizzle, so block 1 is an immediate offset)
+  const int kx = tile_swz<D>(r32);
+  int koff[KSTEPS];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) koff[s] = r32 * ROWB + (((2 * s + g) ^ kx) * 16);
-  // V (transposing read): block beta = lane/16, i = lane%16 = 4*ee + aa
+  for (int s = 0; s < KSTEPS; ++s) koff[s] = r32 * ROWB + (((2 * s + g) ^ kx) * 16);
+  // V (transposing read): block beta = lane/16, i = lane%16 = 4*ee + aa reads
+  // key 16t + 8h + 4*vg + ee, columns dblk*32 + 16*(beta&1) + 4*aa .. +3; the
+  // swizzle of that key does not depend on t, so t is an immediate offset
   const int beta = lane >> 4, ee = (lane & 15) >> 2, aa = lane & 3;
   const int vg = beta >> 1;
-  const int vx = (2 * ee) | vg;
   const int vs0 = 2 * (beta & 1) + (aa >> 1);
-  int voff[2];
+  int voff[DBLK][2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par)
-    voff[par] = (4 * vg + ee) * ROWB + (((4 * par + vs0) ^ vx) * 16) + (aa & 1) * 8;
+  for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int key = 8 * h + 4 * vg + ee;
+      voff[db][h] = key * ROWB + (((4 * db + vs0) ^ tile_swz<D>(key)) * 16) + (aa & 1) * 8;
+    }
 
   // ---- online softmax state ----
   const float c = p.scale_log2;
@@ -225,49 +265,34 @@ fa_fwd_kernel(FwdParams p) {
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) oacc[i] = f32x16{};
 
-  auto compute_tile = [&](const HCP_LDS(char)* Ks, int n0) {
-    if (CAUSAL && n0 > wave_last) return;  // whole tile above this wave's diagonal
-    const HCP_LDS(char)* Vs = Ks + TILEB;
-    // S^T = K Q^T
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      const int o = koff[s & 3] + (s >> 2) * 128;
-      const V8 k0 = lds_read16<V8>(Ks + o);
-      const V8 k1 = lds_read16<V8>(Ks + o + 32 * ROWB);
-      s0 = E::mfma32(k0, qf[s], s0);
-      s1 = E::mfma32(k1, qf[s], s1);
-    }
-    // masking on ragged / diagonal tiles (wave-uniform branch)
+  // One 32-key half of a tile: mask, lazy-rescale check, exp, P^T fragments.
+  // The check needs only this lane's values and a wave vote; the row pair's
+  // exact max (lane ^ 32) is formed only on the rare rescale path.
+  auto softmax_half = [&](f32x16& sh, int n0, int half, V8* pf) __attribute__((always_inline)) {
     const bool ragged = n0 + BN > kv_len;
     const bool diag = CAUSAL && (n0 + BN - 1 > off + wave_q0);
     if (ragged || diag) {
       const int lim_r = kv_len - 1 - n0;
       const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
       const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
-      const int lim = lim_r < lim_c ? lim_r : lim_c;
+      const int lim = (lim_r < lim_c ? lim_r : lim_c) - 32 * half;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-        if (kk > lim) s0[r] = -INFINITY;
-        if (kk + 32 > lim) s1[r] = -INFINITY;
+        if (kk > lim) sh[r] = -INFINITY;
       }
     }
-    // row max: max3 tree over 32 values, then the other half of the row
-    float m4[4];
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int b = 4 * q4;
-      float a = __builtin_fmaxf(__builtin_fmaxf(s0[b], s0[b + 1]), s0[b + 2]);
-      a = __builtin_fmaxf(__builtin_fmaxf(a, s0[b + 3]), s1[b]);
-      a = __builtin_fmaxf(__builtin_fmaxf(a, s1[b + 1]), s1[b + 2]);
-      m4[q4] = __builtin_fmaxf(a, s1[b + 3]);
-    }
-    float mx = __builtin_fmaxf(__builtin_fmaxf(m4[0], m4[1]), __builtin_fmaxf(m4[2], m4[3]));
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-    const float mxs = mx * c;
-    if (__any(mxs > m_ref + kRescaleThresh)) {
-      const float m_new = __builtin_fmaxf(m_ref, mxs);
+    float a0 = __builtin_fmaxf(__builtin_fmaxf(sh[0], sh[1]), sh[2]);
+    float a1 = __builtin_fmaxf(__builtin_fmaxf(sh[3], sh[4]), sh[5]);
+    float a2 = __builtin_fmaxf(__builtin_fmaxf(sh[6], sh[7]), sh[8]);
+    float a3 = __builtin_fmaxf(__builtin_fmaxf(sh[9], sh[10]), sh[11]);
+    float a4 = __builtin_fmaxf(__builtin_fmaxf(sh[12], sh[13]), sh[14]);
+    a0 = __builtin_fmaxf(__builtin_fmaxf(a0, a1), a2);
+    a3 = __builtin_fmaxf(__builtin_fmaxf(a3, a4), sh[15]);
+    const float mh = __builtin_fmaxf(a0, a3);
+    if (__any(mh * c > m_ref + kRescaleThresh)) {
+      const float mrow = __builtin_fmaxf(mh, __shfl_xor(mh, 32)) * c;
+      const float m_new = __builtin_fmaxf(m_ref, mrow);
       const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
       l_run *= alpha;
 #pragma unroll
@@ -275,44 +300,70 @@ fa_fwd_kernel(FwdParams p) {
       m_ref = m_new;
     }
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sh[r] = fast_exp2(__builtin_fmaf(sh[r], c, -m_use));
     float rs = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s0[r] = fast_exp2(__builtin_fmaf(s0[r], c, -m_use));
-      s1[r] = fast_exp2(__builtin_fmaf(s1[r], c, -m_use));
-    }
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) rs += (s0[r] + s0[r + 1]) + (s1[r] + s1[r + 1]);
+    for (int r = 0; r < 16; r += 4) rs += (sh[r] + sh[r + 1]) + (sh[r + 2] + sh[r + 3]);
     l_run += rs;
-    // P^T fragments: step t uses S^T block t/2, registers 8(t%2)..+7
-    V8 pf[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const f32x16& sb = (t < 2) ? s0 : s1;
-      const int b = 8 * (t & 1);
+    for (int t = 0; t < 2; ++t) {
+      const int b = 8 * t;
       u32x4 w;
-      w[0] = pack2<T>(sb[b + 0], sb[b + 1]);
-      w[1] = pack2<T>(sb[b + 2], sb[b + 3]);
-      w[2] = pack2<T>(sb[b + 4], sb[b + 5]);
-      w[3] = pack2<T>(sb[b + 6], sb[b + 7]);
+      w[0] = pack2<T>(sh[b + 0], sh[b + 1]);
+      w[1] = pack2<T>(sh[b + 2], sh[b + 3]);
+      w[2] = pack2<T>(sh[b + 4], sh[b + 5]);
+      w[3] = pack2<T>(sh[b + 6], sh[b + 7]);
       pf[t] = as_vec8<V8>(w);
     }
-    // O^T += V^T P^T
+  };
+
+  // O^T += V^T P^T for PV steps t (16 keys each) of one half
+  auto pv_half = [&](const HCP_LDS(char)* Vs, int half, const V8* pf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
-      const int vb = voff[db & 1] + (db >> 1) * 128;
+    for (int tt = 0; tt < 2; ++tt) {
+      const int t = 2 * half + tt;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const i16x4 lo = lds_read_tr(Vs + vb + (16 * t) * ROWB);
-        const i16x4 hi = lds_read_tr(Vs + vb + (16 * t + 8) * ROWB);
+      for (int db = 0; db < DBLK; ++db) {
+        const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
+        const i16x4 hi = lds_read_tr(Vs + voff[db][1] + (16 * t) * ROWB);
         u32x4 w;
         w[0] = __builtin_bit_cast(u32x2, lo)[0];
         w[1] = __builtin_bit_cast(u32x2, lo)[1];
         w[2] = __builtin_bit_cast(u32x2, hi)[0];
         w[3] = __builtin_bit_cast(u32x2, hi)[1];
-        oacc[db] = E::mfma32(as_vec8<V8>(w), pf[t], oacc[db]);
+        oacc[db] = E::mfma32(as_vec8<V8>(w), pf[tt], oacc[db]);
       }
     }
+  };
+
+  auto qk_block = [&](const HCP_LDS(char)* Ks, int blk) __attribute__((always_inline)) {
+    f32x16 sb = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      sb = E::mfma32(lds_read16<V8>(Ks + koff[s] + blk * 32 * ROWB), qf[s], sb);
+    return sb;
+  };
+
+  // One tile: QK of both 32-key blocks, then per half softmax and PV.  The
+  // wave raises its issue priority while it feeds the matrix pipe, so the
+  // other wave on the SIMD fills the gaps with its softmax VALU work.
+  auto tile_step = [&](const HCP_LDS(char)* Ks, int n0) __attribute__((always_inline)) {
+    if (CAUSAL && n0 > wave_last) return;  // whole tile above this wave's diagonal
+    const HCP_LDS(char)* Vs = Ks + TILEB;
+    __builtin_amdgcn_s_setprio(HCP_MFMA_PRIO);
+    f32x16 s0 = qk_block(Ks, 0);
+    f32x16 s1 = qk_block(Ks, 1);
+    __builtin_amdgcn_s_setprio(0);
+    V8 pf0[2], pf1[2];
+    softmax_half(s0, n0, 0, pf0);
+    __builtin_amdgcn_s_setprio(HCP_MFMA_PRIO);
+    pv_half(Vs, 0, pf0);
+    __builtin_amdgcn_s_setprio(0);
+    softmax_half(s1, n0, 1, pf1);
+    __builtin_amdgcn_s_setprio(HCP_MFMA_PRIO);
+    pv_half(Vs, 1, pf1);
+    __builtin_amdgcn_s_setprio(0);
   };
 
   HCP_LDS(char)* A = (HCP_LDS(char)*)(bufA);
@@ -329,14 +380,14 @@ fa_fwd_kernel(FwdParams p) {
       issue_tile(it + 1, B);
       if (it + 2 < ntiles) fetch_blocks(it + 2);
     }
-    compute_tile(A, it * BN);
+    tile_step(A, it * BN);
     __syncthreads();
     if (it + 1 >= ntiles) break;
     if (it + 2 < ntiles) {
       issue_tile(it + 2, A);
       if (it + 3 < ntiles) fetch_blocks(it + 3);
     }
-    compute_tile(B, (it + 1) * BN);
+    tile_step(B, (it + 1) * BN);
     __syncthreads();
   }
 

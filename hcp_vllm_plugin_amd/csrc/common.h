@@ -6,7 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/hcp_mi355x.h"
+#include "hcp_mi355x.h"  // include/ is on the build's include path
 
 namespace hcp {
 

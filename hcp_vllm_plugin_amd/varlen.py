@@ -82,6 +82,7 @@ def segment_contiguous(k: torch.Tensor, v: torch.Tensor, start: int = 0,
     """Segment over tokens ``[start, start+length)`` of k/v ``[T, Hkv, D]``."""
     if k.shape != v.shape or k.stride() != v.stride():
         raise ValueError("k and v must share shape and strides")
+    _check_kv_layout(k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), 0, k.element_size())
     if k.stride(-1) != 1:
         raise ValueError("k/v head_dim must be contiguous")
     n = k.shape[0] - start if length is None else length
@@ -100,6 +101,17 @@ def segment_contiguous(k: torch.Tensor, v: torch.Tensor, start: int = 0,
     return s
 
 
+def _check_kv_layout(k_addr: int, v_addr: int, stride_tok: int, stride_head: int,
+                     stride_block: int, esize: int) -> None:
+    """Kernel loadability: 16-byte aligned rows, token stride below 2^24 elements."""
+    if k_addr % 16 or v_addr % 16:
+        raise ValueError("k/v base addresses must be 16-byte aligned")
+    if (stride_tok * esize) % 16 or (stride_head * esize) % 16 or (stride_block * esize) % 16:
+        raise ValueError("k/v strides must be multiples of 16 bytes")
+    if not 0 < stride_tok < (1 << 24):
+        raise ValueError("k/v token stride must be in (0, 2^24) elements")
+
+
 def segment_paged(pc: PagedCache, block_table_row: torch.Tensor, start: int,
                   length: int) -> KvSegment:
     """Segment over tokens ``[start, start+length)`` of one request's paged KV.
@@ -109,6 +121,12 @@ def segment_paged(pc: PagedCache, block_table_row: torch.Tensor, start: int,
     """
     if block_table_row.dtype != torch.int32 or block_table_row.stride(-1) != 1:
         raise ValueError("block table row must be contiguous int32")
+    _check_kv_layout(pc.k_addr, pc.v_addr, pc.stride_tok, pc.stride_head, pc.stride_block,
+                     pc.cache.element_size())
+    if pc.block_size <= 0 or pc.block_size & (pc.block_size - 1):
+        raise ValueError("block_size must be a power of two")
+    if start < 0 or length < 0:
+        raise ValueError("negative segment start/length")
     nblk = (start + length + pc.block_size - 1) // pc.block_size
     if length > 0 and nblk > block_table_row.shape[0]:
         raise ValueError("segment extends past the block-table row")
