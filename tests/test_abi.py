@@ -1,0 +1,204 @@
+"""CPU checks of the C-ABI library (no GPU needed, no kernel launched).
+
+* libhcp_mi355x.so loads and exports every function include/hcp_mi355x.h
+  declares, with the declared ABI version.
+* The host-side planners (hcp_plan_varlen_tiles, hcp_plan_decode_splits,
+  hcp_decode_workspace_bytes) run on the CPU: their output is checked against
+  brute-force enumeration of the work they describe.
+* Argument validation returns the documented status codes (and text through
+  hcp_last_error) before anything reaches the GPU.
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from hcp_vllm_plugin_amd import _lib
+from hcp_vllm_plugin_amd._lib import DecodeSplit, KvSegment, VarlenEntry
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hcp_mi355x.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(hcp_[a-z_0-9]+)\s*\(", src, re.M)
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built: run __graft_entry__.build()")
+    return _lib.lib()
+
+
+def test_header_declares_what_the_wrapper_binds():
+    assert sorted(header_functions()) == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_header_symbol(L):
+    names = header_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(L, n), n
+    # and they are real dynamic exports with C linkage (no C++ mangling)
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    for n in names:
+        assert n in exported, n
+
+
+def test_abi_version(L):
+    assert L.hcp_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layouts_match_header():
+    # hcp_kv_segment: 3 u64 + 5 i64 + 2 i32 = 72 bytes; entry adds 3 i64
+    assert ctypes.sizeof(KvSegment) == 72
+    assert ctypes.sizeof(VarlenEntry) == 96
+    assert ctypes.sizeof(DecodeSplit) == 16
+    assert VarlenEntry.kv.offset == 24
+
+
+def _entry(q_start, q_len, off, kv_len, start=0):
+    e = VarlenEntry()
+    e.q_start, e.q_len, e.causal_offset = q_start, q_len, off
+    e.kv.k_addr = e.kv.v_addr = 0x1000
+    e.kv.stride_tok, e.kv.stride_head = 512, 128
+    e.kv.start, e.kv.len = start, kv_len
+    return e
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_plan_varlen_tiles_covers_every_block_longest_first(L, causal):
+    specs = [(0, 300, 0, 300), (300, 1, 5, 900), (301, 129, 40, 200), (430, 0, 0, 10),
+             (430, 700, -50, 700), (1130, 256, 10000, 64)]
+    ents = [_entry(*s) for s in specs]
+    arr = (VarlenEntry * len(ents))(*ents)
+    bm = L.hcp_varlen_block_m(128, _lib.DTYPE_BF16)
+    assert bm > 0
+    need = sum(-(-s[1] // bm) for s in specs)
+    tiles = (ctypes.c_int32 * (2 * need))()
+    n = L.hcp_plan_varlen_tiles(ctypes.addressof(arr), len(ents), causal, bm,
+                                ctypes.addressof(tiles), need)
+    assert n == need
+    got = [(tiles[2 * i], tiles[2 * i + 1]) for i in range(n)]
+    want = {(e, b) for e, s in enumerate(specs) for b in range(-(-s[1] // bm))}
+    assert set(got) == want and len(got) == len(want)
+
+    def cost(e, b):
+        q_start, q_len, off, kv_len = specs[e]
+        if not causal:
+            return kv_len
+        # keys visible to the block's last row, by enumeration
+        last = min((b + 1) * bm, q_len + bm) - 1
+        return sum(1 for j in range(kv_len) if j <= off + last)
+
+    costs = [cost(e, b) for e, b in got]
+    assert costs == sorted(costs, reverse=True)
+    # too small a cap is reported, not overrun
+    rc = L.hcp_plan_varlen_tiles(ctypes.addressof(arr), len(ents), causal, bm,
+                                 ctypes.addressof(tiles), need - 1)
+    assert rc == _lib.HCP_EWORKSPACE
+    assert b"need" in L.hcp_last_error()
+
+
+def test_plan_decode_splits_partition_each_segment(L):
+    # 3 sequences: (kv lens of its entries)
+    seqs = [[4096, 700], [0, 1], [33, 2048, 5]]
+    ents, seq_of = [], []
+    for s, lens in enumerate(seqs):
+        for ln in lens:
+            ents.append(_entry(s, 1, 0, ln))
+            seq_of.append(s)
+    arr = (VarlenEntry * len(ents))(*ents)
+    sq = (ctypes.c_int32 * len(ents))(*seq_of)
+    split = 256
+    cap = sum(-(-e.kv.len // split) for e in ents)
+    out = (DecodeSplit * cap)()
+    starts = (ctypes.c_int32 * (len(seqs) + 1))()
+    n = L.hcp_plan_decode_splits(ctypes.addressof(arr), len(ents), ctypes.addressof(sq),
+                                 len(seqs), 0, split, ctypes.addressof(out), cap,
+                                 ctypes.addressof(starts))
+    assert n == cap
+    sp = [(out[i].entry, out[i].key_begin, out[i].key_end) for i in range(n)]
+    # every key of every entry in exactly one split, each split <= split_tokens
+    for ei, e in enumerate(ents):
+        keys = []
+        for en, b, k in sp:
+            if en == ei:
+                assert 0 < k - b <= split
+                keys.extend(range(b, k))
+        assert keys == list(range(e.kv.len))
+    # partial slots of sequence s are exactly the splits of its entries
+    for s in range(len(seqs)):
+        mine = [i for i, (en, _, _) in enumerate(sp) if seq_of[en] == s]
+        assert mine == list(range(starts[s], starts[s + 1]))
+    assert starts[len(seqs)] == n
+
+
+def test_plan_decode_splits_causal_limit_and_errors(L):
+    ents = [_entry(0, 1, 99, 1000)]
+    arr = (VarlenEntry * 1)(*ents)
+    sq = (ctypes.c_int32 * 1)(0)
+    out = (DecodeSplit * 8)()
+    starts = (ctypes.c_int32 * 2)()
+    n = L.hcp_plan_decode_splits(ctypes.addressof(arr), 1, ctypes.addressof(sq), 1, 1, 64,
+                                 ctypes.addressof(out), 8, ctypes.addressof(starts))
+    assert n == 2 and out[1].key_end == 100  # keys j <= 99
+    # q_len != 1 is rejected
+    ents[0].q_len = 2
+    arr = (VarlenEntry * 1)(*ents)
+    rc = L.hcp_plan_decode_splits(ctypes.addressof(arr), 1, ctypes.addressof(sq), 1, 0, 64,
+                                  ctypes.addressof(out), 8, ctypes.addressof(starts))
+    assert rc == _lib.HCP_EINVAL
+    assert b"q_len" in L.hcp_last_error()
+
+
+def test_decode_workspace_bytes(L):
+    n, h, d = 37, 28, 128
+    b = L.hcp_decode_workspace_bytes(n, h, d)
+    o = n * h * d * 4
+    assert b >= o + n * h * 4 and b - (o + n * h * 4) < 256
+    assert L.hcp_decode_workspace_bytes(0, h, d) == 0
+
+
+def _fwd(L, **kw):
+    a = dict(q=16, k=16, v=16, out=16, lse=16, tq=4, tk=4, h=28, hkv=4, d=128,
+             st=8, causal=1, off=0, dtype=_lib.DTYPE_BF16, scale=0.088)
+    a.update(kw)
+    s = a["st"]
+    return L.hcp_attn_fwd_lse(a["q"], a["k"], a["v"], a["out"], a["lse"], a["tq"], a["tk"],
+                              a["h"], a["hkv"], a["d"], s * a["h"], s, s * a["hkv"], s,
+                              s * a["hkv"], s, s * a["h"], s, a["tq"], a["scale"],
+                              a["causal"], a["off"], a["dtype"], None)
+
+
+def test_argument_validation_status_codes(L):
+    assert _fwd(L, h=6, hkv=4) == _lib.HCP_EINVAL
+    assert b"multiple" in L.hcp_last_error()
+    assert _fwd(L, d=96) == _lib.HCP_EUNSUPPORTED
+    assert _fwd(L, dtype=_lib.DTYPE_F32) == _lib.HCP_EUNSUPPORTED
+    assert _fwd(L, tq=-1) == _lib.HCP_EINVAL
+    assert _fwd(L, scale=float("nan")) == _lib.HCP_EINVAL
+    assert _fwd(L, q=None) == _lib.HCP_EINVAL
+    assert _fwd(L, q=24) == _lib.HCP_EINVAL          # not 16-byte aligned
+    assert _fwd(L, st=12) == _lib.HCP_EINVAL         # stride not a multiple of 8
+    assert _fwd(L, tq=0) == _lib.HCP_OK              # nothing to do, nothing launched
+    rc = L.hcp_merge_attn_states(16, 8, 8, 7, None, 0, 16, 8, 8, 1, 16, 4, 16, 8, 8, 1, 16, 4,
+                                 4, 1, 8, None)
+    assert rc == _lib.HCP_EUNSUPPORTED  # out dtype 7
+    rc = L.hcp_merge_attn_states(16, 8, 8, 1, None, 0, 16, 8, 8, 1, 16, 4, 16, 8, 8, 1, 16, 4,
+                                 4, 1, 12, None)
+    assert rc == _lib.HCP_EUNSUPPORTED  # head_dim 12
+
+
+def test_check_raises_runtime_error_with_library_text(L):
+    rc = _fwd(L, d=96)
+    with pytest.raises(RuntimeError, match="EUNSUPPORTED.*head_dim 96"):
+        _lib.check(rc, "hcp_attn_fwd_lse")
