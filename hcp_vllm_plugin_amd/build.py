@@ -27,6 +27,9 @@ HIPCC_FLAGS = [
     "-fPIC",
     # packed-FP32 VALU forms are kept out of the generated code on purpose
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results stay in arch VGPRs: the softmax reads the score tiles with
+    # VALU ops, which cannot take AGPR operands
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",

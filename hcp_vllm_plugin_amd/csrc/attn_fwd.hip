@@ -10,12 +10,13 @@
 // (:119-125,186), P rounded to the input dtype before the PV product (:133),
 // lse = m * ln2 + ln(l) (:140), GQA head map h / G (:64).
 //
-// Design (one workgroup = 4 waves = 128 query rows of one head, 32 per wave):
+// Design (one workgroup = 4 waves = 128 query rows of one head, 32 per wave;
+// two workgroups per CU, i.e. two waves per SIMD):
 //  * S^T = K Q^T on v_mfma_f32_32x32x16_{bf16,f16}: K (keys x D) is the A
 //    operand read from LDS, Q^T the B operand held in registers for the whole
 //    kernel.  In the 32x32 accumulator layout a lane owns one column, so each
 //    lane owns ONE query row and 16 of its keys per 32-key block: the row max
-//    is an in-register max3 tree plus one exchange with lane ^ 32, and the
+//    is an in-register max3 chain plus one exchange with lane ^ 32, and the
 //    row sum stays a per-lane partial until the epilogue.
 //  * O^T = V^T P^T on the same MFMA: P^T comes straight from the S^T
 //    registers (the key order inside the k dimension is a free permutation);
@@ -23,24 +24,33 @@
 //    transposing LDS read ds_read_b64_tr_b16: inside each 16-lane block,
 //    lane 4e+a reads 4 consecutive d of key kbase+e and every lane receives 4
 //    keys of one d column.
+//  * Software pipeline over 64-key tiles: iteration n computes S(n+1) on the
+//    matrix pipe while the VALU turns S(n) into P(n) (phase A), then O +=
+//    V(n)^T P(n)^T while the VALU sums P(n) and takes the max of S(n+1)
+//    (phase B).  Each MFMA step carries its own share of VALU work and its
+//    LDS reads a few MFMAs ahead, written out in order and pinned with
+//    scheduling barriers, so the softmax runs under the MFMAs instead of
+//    between them.
 //  * K and V tiles (64 keys x D, row-major, 16-byte slots XOR-swizzled by
 //    2*(row&3) | (row>>2 & 1) so both the K reads and the transposing V reads
-//    are bank-conflict free) are filled by global_load_lds_dwordx4: HBM/L2 ->
-//    LDS with no register staging and no VALU work.  Two tile buffers are
-//    separate __shared__ objects and the key loop is unrolled by two, so the
-//    loads for tile n+1 stay in flight while tile n is computed (one barrier
-//    per tile).
+//    are bank-conflict free) go HBM/L2 -> LDS with buffer_load ... lds (no
+//    register staging, no VALU work), one load instruction every four MFMAs
+//    of the phase that does not read that buffer.  Two K and two V buffers:
+//    iteration n reads K(n+1), V(n) and fills K(n+2), V(n+1); one barrier per
+//    tile.
 //  * Lazy rescale: the running max used as the exponent reference is only
 //    raised when some row's tile max exceeds it by more than 2^8; otherwise P
 //    values are bounded by 256 and the O rescale (64 multiplies per lane) is
 //    skipped.  The result is exact: O, l and lse all use the same reference.
 //  * Causal tiles above a wave's diagonal are skipped; masking runs only on
-//    diagonal and ragged tiles.  Ragged tiles clamp key rows into the segment
-//    (the clamped rows are masked in S, and their finite V values meet P = 0),
-//    so no load goes out of bounds and no load is predicated.
+//    diagonal and ragged tiles.  A ragged last tile is bounded by its buffer
+//    descriptor (rows past the segment read as zeros and are masked), so no
+//    load leaves the segment and none is predicated.
 //  * The local (paged) segment is read in place through the block table
 //    (hcp_kv_segment), replacing the per-request gather copy of
-//    ring_backend.py:617-624; block ids are fetched two tiles ahead.
+//    ring_backend.py:617-624; block ids are fetched ahead of the tile loads.
+#include <type_traits>
+
 #include "params.h"
 
 namespace hcp {
@@ -48,8 +58,14 @@ namespace hcp {
 #ifndef HCP_MFMA_PRIO
 #define HCP_MFMA_PRIO 3
 #endif
+#ifndef HCP_FWD_WAVES_PER_EU
+#define HCP_FWD_WAVES_PER_EU 2
+#endif
 
 constexpr float kRescaleThresh = 8.0f;  // log2 units: P <= 2^8 between rescales
+// word 3 of a raw (stride 0) buffer descriptor on gfx9-family parts:
+// DATA_FORMAT = 32 bit, no swizzle, bounds checked against num_records
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define HCP_LDS(T) __attribute__((address_space(3))) T
@@ -84,20 +100,24 @@ __device__ __forceinline__ i16x4 lds_read_tr(const HCP_LDS(char)* p) {
 
 template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
-                          amdgpu_waves_per_eu(2, 2))) void
+                          amdgpu_waves_per_eu(HCP_FWD_WAVES_PER_EU, HCP_FWD_WAVES_PER_EU))) void
 fa_fwd_kernel(FwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::vec8;
   constexpr int BM = kFwdBM, BN = kFwdBN;
-  constexpr int ROWB = D * 2;                  // bytes per tile row
-  constexpr int TILEB = BN * ROWB;             // bytes per K (or V) tile
+  constexpr int ROWB = D * 2;                     // bytes per tile row
+  constexpr int TILEB = BN * ROWB;                // bytes per K (or V) tile
   constexpr int NI = TILEB / (kFwdThreads * 16);  // direct loads per thread per tile
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
   static_assert(D == 64 || D == 128, "head_dim");
 
-  __shared__ __attribute__((aligned(1024))) char bufA[2 * TILEB];  // K | V
-  __shared__ __attribute__((aligned(1024))) char bufB[2 * TILEB];
+  // Two K tiles and two V tiles.  Iteration n reads K(n+1) and V(n) while the
+  // loads of K(n+2) and V(n+1) land in the other buffers.
+  __shared__ __attribute__((aligned(1024))) char bufK0[TILEB];
+  __shared__ __attribute__((aligned(1024))) char bufK1[TILEB];
+  __shared__ __attribute__((aligned(1024))) char bufV0[TILEB];
+  __shared__ __attribute__((aligned(1024))) char bufV1[TILEB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -152,18 +172,29 @@ fa_fwd_kernel(FwdParams p) {
   if (n_end < 0) n_end = 0;
   const int ntiles = static_cast<int>((n_end + BN - 1) / BN);
   const int64_t wave_q0 = static_cast<int64_t>(qb) * BM + wave * 32;
-  const int64_t wave_last = CAUSAL ? off + wave_q0 + 31 : static_cast<int64_t>(kv_len) - 1;
+  // tiles this wave computes: all of the workgroup's tiles up to its diagonal;
+  // a wave without valid query rows computes none (it still loads and syncs)
+  int wtiles = ntiles;
+  if (wave_q0 >= q_len) {
+    wtiles = 0;
+  } else if (CAUSAL) {
+    const int64_t wave_last = off + wave_q0 + 31;
+    const int64_t wt = wave_last < 0 ? 0 : wave_last / BN + 1;
+    wtiles = wt < ntiles ? static_cast<int>(wt) : ntiles;
+  }
 
   // ---- direct tile loads: lane's row / chunk for load instruction i ----
-  // instruction i of wave w fills LDS bytes [(w*NI+i)*1024, +1024)
-  int lrow[NI];
-  int lchunk[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int o = (wave * NI + i) * 1024 + lane * 16;
-    lrow[i] = o / ROWB;
-    lchunk[i] = ((o % ROWB) / 16) ^ tile_swz<D>(lrow[i]);
-  }
+  // instruction i of wave w fills LDS bytes [(w*NI+i)*1024, +1024) of a tile
+  // Load instruction i of wave w fills LDS bytes [(w*NI+i)*1024, +1024) of a
+  // tile: lane l covers tile row lrow0 + i*RPI, 16-byte chunk lchunk(i).
+  // Rows and chunks are recomputed where needed (cheap) instead of being
+  // kept in registers for the whole kernel.
+  constexpr int RPI = 1024 / ROWB;  // tile rows per load instruction
+  const int lrow0 = wave * NI * RPI + (lane * 16) / ROWB;
+  auto lrow = [&](int i) __attribute__((always_inline)) { return lrow0 + i * RPI; };
+  auto lchunk = [&](int i) __attribute__((always_inline)) {
+    return (((lane * 16) % ROWB) / 16) ^ tile_swz<D>(lrow(i));
+  };
   const int64_t rowb_g = e.kv.stride_tok * 2;  // bytes between tokens in HBM
   const char* kseg;
   const char* vseg;
@@ -181,16 +212,18 @@ fa_fwd_kernel(FwdParams p) {
     kseg = reinterpret_cast<const char*>(e.kv.k_addr) + base;
     vseg = reinterpret_cast<const char*>(e.kv.v_addr) + base;
   }
-  // paged: block ids of the lane's rows for the next tile to be issued
-  int bnext[NI];
 
-  auto fetch_blocks = [&](int tile_idx) __attribute__((always_inline)) {
+  // paged: block ids of the lane's rows.  Tile j's K is issued at iteration
+  // j-2 and its V at iteration j-1, so three tiles' ids are live: bid_v (tile
+  // n+1), bid_k (tile n+2) and bid_f (tile n+3, fetched during iteration n).
+  int bid_v[NI], bid_k[NI], bid_f[NI];
+  auto fetch_blocks = [&](int tile_idx, int (&dst)[NI]) __attribute__((always_inline)) {
     if constexpr (PAGED) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        int key = tile_idx * BN + lrow[i];
+        int key = tile_idx * BN + lrow(i);
         key = key < kv_len ? key : kv_len - 1;
-        bnext[i] = bt[(e.kv.start + key) >> bs_shift];
+        dst[i] = bt[(e.kv.start + key) >> bs_shift];
       }
     }
   };
@@ -200,40 +233,69 @@ fa_fwd_kernel(FwdParams p) {
   const uint32_t rowb32 = static_cast<uint32_t>(rowb_g);
   uint32_t goff[NI];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) goff[i] = lrow[i] * rowb32 + lchunk[i] * 16u;
+  for (int i = 0; i < NI; ++i) goff[i] = lrow(i) * rowb32 + lchunk(i) * 16u;
 
-  auto issue_tile = [&](int tile_idx, HCP_LDS(char)* dst) __attribute__((always_inline)) {
+  // Issue the global->LDS loads of one tile of K or V.  Ragged tiles clamp
+  // their key rows into the segment (those rows are masked in S, and their
+  // finite V values meet P = 0), so no load leaves the segment.
+  auto issue = [&](const char* seg, int tile_idx, const int (&bids)[NI], HCP_LDS(char)* dst)
+      __attribute__((always_inline)) {
     const int n0 = tile_idx * BN;
     const bool ragged = n0 + BN > kv_len;
     if constexpr (PAGED) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        int key = n0 + lrow[i];
+        int key = n0 + lrow(i);
         if (ragged) key = key < kv_len ? key : kv_len - 1;
         const int64_t x = e.kv.start + key;
         const int64_t go =
-            static_cast<int64_t>(bnext[i]) * blockb + (x & bs_mask) * rowb_g + lchunk[i] * 16;
-        HCP_LDS(char)* l = dst + (wave * NI + i) * 1024;
-        lds_load16(kseg + go, l);
-        lds_load16(vseg + go, l + TILEB);
+            static_cast<int64_t>(bids[i]) * blockb + (x & bs_mask) * rowb_g + lchunk(i) * 16;
+        lds_load16(seg + go, dst + (wave * NI + i) * 1024);
       }
     } else {
-      const char* kt = kseg + static_cast<int64_t>(n0) * rowb_g;
-      const char* vt = vseg + static_cast<int64_t>(n0) * rowb_g;
+      // MUBUF form (buffer_load ... lds) over a descriptor rebased per tile:
+      // 32-bit offsets never overflow, and unlike the FLAT-encoded
+      // global_load_lds it leaves the compiler exact LDS-read wait counts
+      const char* base = seg + static_cast<int64_t>(n0) * rowb_g;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(base), 0, 0x7fffffff, kBufferRsrcWord3);
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         uint32_t o = goff[i];
         if (ragged) {
-          const int key = n0 + lrow[i];
+          const int key = n0 + lrow(i);
           const int kc = key < kv_len ? key : kv_len - 1;
-          o = static_cast<uint32_t>(kc - n0) * rowb32 + lchunk[i] * 16u;
+          o = static_cast<uint32_t>(kc - n0) * rowb32 + lchunk(i) * 16u;
         }
-        HCP_LDS(char)* l = dst + (wave * NI + i) * 1024;
-        lds_load16(kt + o, l);
-        lds_load16(vt + o, l + TILEB);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
+            static_cast<int>(o), 0, 0, 0);
       }
     }
   };
+
+  // Contiguous segments: a buffer descriptor per (clamped) tile.  Tile
+  // indices past the last tile are clamped to it (such loads fill a buffer
+  // nobody reads); a ragged last tile gets num_records = its valid bytes, so
+  // rows past the segment read as zeros (they are masked in S, and zero V
+  // rows meet P = 0) with no per-lane clamping.
+  auto tile_rsrc = [&](const char* seg, int tile_idx) __attribute__((always_inline)) {
+    const int t = tile_idx < ntiles ? tile_idx : ntiles - 1;
+    const int rows = kv_len - t * BN;
+    const int nrec = rows >= BN ? 0x7fffffff
+                                : static_cast<int>((rows - 1) * rowb_g) + ROWB;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(seg + static_cast<int64_t>(t) * BN * rowb_g), 0, nrec,
+        kBufferRsrcWord3);
+  };
+  auto load_one = [&](__amdgpu_buffer_rsrc_t rs, int i, HCP_LDS(char)* dst)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
+        static_cast<int>(goff[i]), 0, 0, 0);
+  };
+  // load i of a tile is issued under MFMA step LOAD_STEP(i) of a phase
+  constexpr int kLoadEvery = 4;
 
   // ---- LDS read addresses (loop invariant, per lane) ----
   // K (A operand of S^T): row 32*blk + r32, 16-byte chunk 2s+g
@@ -258,38 +320,69 @@ fa_fwd_kernel(FwdParams p) {
     }
 
   // ---- online softmax state ----
+  // m_ref: exponent reference of the row (log2 units), raised only when a
+  // tile's scores exceed it by more than kRescaleThresh, so P <= 2^8.
   const float c = p.scale_log2;
   float m_ref = -INFINITY;
   float l_run = 0.f;
   f32x16 oacc[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) oacc[i] = f32x16{};
+  f32x16 SA[2], SB[2];  // scores of two tiles (ping-pong), 2 x 32 keys each
+  V8 pf[4];             // P^T of the current tile, 16 keys per fragment
 
-  // One 32-key half of a tile: mask, lazy-rescale check, exp, P^T fragments.
-  // The check needs only this lane's values and a wave vote; the row pair's
-  // exact max (lane ^ 32) is formed only on the rare rescale path.
-  auto softmax_half = [&](f32x16& sh, int n0, int half, V8* pf) __attribute__((always_inline)) {
-    const bool ragged = n0 + BN > kv_len;
-    const bool diag = CAUSAL && (n0 + BN - 1 > off + wave_q0);
-    if (ragged || diag) {
-      const int lim_r = kv_len - 1 - n0;
-      const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
-      const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
-      const int lim = (lim_r < lim_c ? lim_r : lim_c) - 32 * half;
+  // S^T = K Q^T of one tile (64 keys) from LDS
+  auto qk = [&](const HCP_LDS(char)* Ks, f32x16 (&S)[2]) __attribute__((always_inline)) {
+    S[0] = f32x16{};
+    S[1] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      S[0] = E::mfma32(lds_read16<V8>(Ks + koff[s]), qf[s], S[0]);
+      S[1] = E::mfma32(lds_read16<V8>(Ks + koff[s] + 32 * ROWB), qf[s], S[1]);
+    }
+  };
+
+  // causal diagonal / ragged masking of tile n (keys n*BN ..): -inf
+  auto needs_mask = [&](int n) __attribute__((always_inline)) {
+    const int n0 = n * BN;
+    return (n0 + BN > kv_len) || (CAUSAL && (n0 + BN - 1 > off + wave_q0));
+  };
+  auto apply_mask = [&](f32x16 (&S)[2], int n) __attribute__((always_inline)) {
+    const int n0 = n * BN;
+    const int lim_r = kv_len - 1 - n0;
+    const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
+    const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
+    const int lim = lim_r < lim_c ? lim_r : lim_c;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-        if (kk > lim) sh[r] = -INFINITY;
+        const int kk = 32 * h + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (kk > lim) S[h][r] = -INFINITY;
       }
+  };
+
+  // lane's max over its 32 scores of a tile (raw, unscaled)
+  auto tile_max = [&](const f32x16 (&S)[2]) __attribute__((always_inline)) {
+    float a[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float a0 = __builtin_fmaxf(__builtin_fmaxf(S[h][0], S[h][1]), S[h][2]);
+      float a1 = __builtin_fmaxf(__builtin_fmaxf(S[h][3], S[h][4]), S[h][5]);
+      float a2 = __builtin_fmaxf(__builtin_fmaxf(S[h][6], S[h][7]), S[h][8]);
+      float a3 = __builtin_fmaxf(__builtin_fmaxf(S[h][9], S[h][10]), S[h][11]);
+      float a4 = __builtin_fmaxf(__builtin_fmaxf(S[h][12], S[h][13]), S[h][14]);
+      a0 = __builtin_fmaxf(__builtin_fmaxf(a0, a1), a2);
+      a3 = __builtin_fmaxf(__builtin_fmaxf(a3, a4), S[h][15]);
+      a[h] = __builtin_fmaxf(a0, a3);
     }
-    float a0 = __builtin_fmaxf(__builtin_fmaxf(sh[0], sh[1]), sh[2]);
-    float a1 = __builtin_fmaxf(__builtin_fmaxf(sh[3], sh[4]), sh[5]);
-    float a2 = __builtin_fmaxf(__builtin_fmaxf(sh[6], sh[7]), sh[8]);
-    float a3 = __builtin_fmaxf(__builtin_fmaxf(sh[9], sh[10]), sh[11]);
-    float a4 = __builtin_fmaxf(__builtin_fmaxf(sh[12], sh[13]), sh[14]);
-    a0 = __builtin_fmaxf(__builtin_fmaxf(a0, a1), a2);
-    a3 = __builtin_fmaxf(__builtin_fmaxf(a3, a4), sh[15]);
-    const float mh = __builtin_fmaxf(a0, a3);
+    return __builtin_fmaxf(a[0], a[1]);
+  };
+
+  // Lazy rescale: raise m_ref only if some row's tile max exceeds it by more
+  // than the threshold (a wave vote); the row pair (lane, lane^32) then agrees
+  // on the new reference.  O and l hold everything up to the previous tile.
+  auto check_rescale = [&](float mh) __attribute__((always_inline)) {
     if (__any(mh * c > m_ref + kRescaleThresh)) {
       const float mrow = __builtin_fmaxf(mh, __shfl_xor(mh, 32)) * c;
       const float m_new = __builtin_fmaxf(m_ref, mrow);
@@ -299,30 +392,43 @@ fa_fwd_kernel(FwdParams p) {
       for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
       m_ref = m_new;
     }
+  };
+
+  // P = exp2(c*S - m_ref), in place (fp32, kept for the row sum), and the
+  // P^T fragments in the input dtype
+  auto expo = [&](f32x16 (&S)[2]) __attribute__((always_inline)) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sh[r] = fast_exp2(__builtin_fmaf(sh[r], c, -m_use));
-    float rs = 0.f;
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int r = 0; r < 16; r += 4) rs += (sh[r] + sh[r + 1]) + (sh[r + 2] + sh[r + 3]);
-    l_run += rs;
+      for (int r = 0; r < 16; ++r) S[h][r] = fast_exp2(__builtin_fmaf(S[h][r], c, -m_use));
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int b = 8 * t;
-      u32x4 w;
-      w[0] = pack2<T>(sh[b + 0], sh[b + 1]);
-      w[1] = pack2<T>(sh[b + 2], sh[b + 3]);
-      w[2] = pack2<T>(sh[b + 4], sh[b + 5]);
-      w[3] = pack2<T>(sh[b + 6], sh[b + 7]);
-      pf[t] = as_vec8<V8>(w);
+      for (int t = 0; t < 2; ++t) {
+        const int b = 8 * t;
+        u32x4 w;
+        w[0] = pack2<T>(S[h][b + 0], S[h][b + 1]);
+        w[1] = pack2<T>(S[h][b + 2], S[h][b + 3]);
+        w[2] = pack2<T>(S[h][b + 4], S[h][b + 5]);
+        w[3] = pack2<T>(S[h][b + 6], S[h][b + 7]);
+        pf[2 * h + t] = as_vec8<V8>(w);
+      }
     }
   };
 
-  // O^T += V^T P^T for PV steps t (16 keys each) of one half
-  auto pv_half = [&](const HCP_LDS(char)* Vs, int half, const V8* pf) __attribute__((always_inline)) {
+  auto row_sum = [&](const f32x16 (&S)[2]) __attribute__((always_inline)) {
+    float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int t = 2 * half + tt;
+    for (int r = 0; r < 16; r += 2) {
+      s0 += S[0][r] + S[0][r + 1];
+      s1 += S[1][r] + S[1][r + 1];
+    }
+    return s0 + s1;
+  };
+
+  // O^T += V^T P^T over the tile's 64 keys (4 steps of 16)
+  auto pv = [&](const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int db = 0; db < DBLK; ++db) {
         const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
@@ -332,64 +438,196 @@ fa_fwd_kernel(FwdParams p) {
         w[1] = __builtin_bit_cast(u32x2, lo)[1];
         w[2] = __builtin_bit_cast(u32x2, hi)[0];
         w[3] = __builtin_bit_cast(u32x2, hi)[1];
-        oacc[db] = E::mfma32(as_vec8<V8>(w), pf[tt], oacc[db]);
+        oacc[db] = E::mfma32(as_vec8<V8>(w), pf[t], oacc[db]);
       }
     }
   };
 
-  auto qk_block = [&](const HCP_LDS(char)* Ks, int blk) __attribute__((always_inline)) {
-    f32x16 sb = f32x16{};
+  // One iteration n of the software pipeline, S_cur = scores of tile n
+  // (masked, checked against m_ref), S_nxt receives tile n+1:
+  //   A: S_nxt = K(n+1) Q^T            on MFMA, interleaved with
+  //      P(n) = exp2(c S_cur - m_ref)  on VALU
+  //   B: O += V(n)^T P(n)^T            on MFMA, interleaved with
+  //      l += rowsum P(n), max of S_nxt on VALU
+  //   then the (rare) rescale for tile n+1.
+  // Each phase is one branch-free basic block (on a wave's last tile, A
+  // multiplies a stale LDS tile whose result is discarded); the group
+  // barriers ask the scheduler to alternate MFMA, LDS reads and VALU so the
+  // matrix pipe stays fed while the softmax runs.  The four tile buffers are
+  // distinct __shared__ objects so the compiler can tell the LDS reads from
+  // the global->LDS writes in flight and does not wait for the latter.
+  // ---- the two phases of one pipeline iteration, in explicit order ----
+  // Phase A: S_nxt = K(n+1) Q^T (2*KSTEPS MFMAs, K fragments read from LDS
+  // three MFMAs ahead) while P(n) = exp2(c S_cur - m_ref) and its P^T
+  // fragments are formed, EA scores per MFMA.
+  constexpr int NA = 2 * KSTEPS;  // MFMAs in phase A
+  constexpr int EA = 32 / NA;     // scores exponentiated per phase-A MFMA
+  constexpr int NB = 4 * DBLK;    // MFMAs in phase B
+  constexpr int EB = 32 / NB;     // scores summed / maxed per phase-B MFMA
+  auto phase_a = [&](const HCP_LDS(char)* Ks, f32x16 (&Sc)[2], f32x16 (&Sn)[2],
+                     __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads)
+      __attribute__((always_inline)) {
+    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+    V8 kf[4];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s)
-      sb = E::mfma32(lds_read16<V8>(Ks + koff[s] + blk * 32 * ROWB), qf[s], sb);
-    return sb;
+    for (int j = 0; j < 3; ++j)
+      kf[j] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
+#pragma unroll
+    for (int st = 0; st < NA; ++st) {
+      const int s = st >> 1, blk = st & 1;
+      if (st + 3 < NA) {
+        const int j = st + 3;
+        kf[j & 3] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
+      }
+      Sn[blk] = E::mfma32(kf[st & 3], qf[s], s == 0 ? f32x16{} : Sn[blk]);
+      if (loads && st % kLoadEvery == kLoadEvery / 2 && st / kLoadEvery < NI)
+        load_one(rs, st / kLoadEvery, ldst);
+      // scores st*EA .. st*EA+EA-1 of the current tile: half h, regs r..
+#pragma unroll
+      for (int q = 0; q < EA; q += 2) {
+        const int x = st * EA + q;  // 0..31, even
+        const int h = x >> 4, r = x & 15;
+        const float p0 = fast_exp2(__builtin_fmaf(Sc[h][r], c, -m_use));
+        const float p1 = fast_exp2(__builtin_fmaf(Sc[h][r + 1], c, -m_use));
+        Sc[h][r] = p0;
+        Sc[h][r + 1] = p1;
+        // P^T fragment 2h + (r >> 3) holds regs 8t .. 8t+7 of half h
+        u32x4 w = __builtin_bit_cast(u32x4, pf[2 * h + (r >> 3)]);
+        w[(r & 7) >> 1] = pack2<T>(p0, p1);
+        pf[2 * h + (r >> 3)] = as_vec8<V8>(w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // P(n) is complete here: keep its computation in this phase (all its uses
+    // are in phase B, past the masking branch, where code motion would
+    // otherwise move it and serialise it behind the PV MFMAs)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pf[i]));
+    asm volatile("" : "+v"(Sc[0]), "+v"(Sc[1]));
   };
 
-  // One tile: QK of both 32-key blocks, then per half softmax and PV.  The
-  // wave raises its issue priority while it feeds the matrix pipe, so the
-  // other wave on the SIMD fills the gaps with its softmax VALU work.
-  auto tile_step = [&](const HCP_LDS(char)* Ks, int n0) __attribute__((always_inline)) {
-    if (CAUSAL && n0 > wave_last) return;  // whole tile above this wave's diagonal
-    const HCP_LDS(char)* Vs = Ks + TILEB;
-    __builtin_amdgcn_s_setprio(HCP_MFMA_PRIO);
-    f32x16 s0 = qk_block(Ks, 0);
-    f32x16 s1 = qk_block(Ks, 1);
-    __builtin_amdgcn_s_setprio(0);
-    V8 pf0[2], pf1[2];
-    softmax_half(s0, n0, 0, pf0);
-    __builtin_amdgcn_s_setprio(HCP_MFMA_PRIO);
-    pv_half(Vs, 0, pf0);
-    __builtin_amdgcn_s_setprio(0);
-    softmax_half(s1, n0, 1, pf1);
-    __builtin_amdgcn_s_setprio(HCP_MFMA_PRIO);
-    pv_half(Vs, 1, pf1);
-    __builtin_amdgcn_s_setprio(0);
+  // Phase B: O += V(n)^T P(n)^T (NB MFMAs, transposing V reads two MFMAs
+  // ahead) while l gathers P(n)'s row sum and mh the raw max of S_nxt.
+  auto phase_b = [&](const HCP_LDS(char)* Vs, const f32x16 (&Sc)[2], const f32x16 (&Sn)[2],
+                     float& mh, __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads)
+      __attribute__((always_inline)) {
+    u32x4 vf[3];
+    auto vread = [&](int j) __attribute__((always_inline)) {
+      const int t = j / DBLK, db = j % DBLK;
+      const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
+      const i16x4 hi = lds_read_tr(Vs + voff[db][1] + (16 * t) * ROWB);
+      u32x4 w;
+      w[0] = __builtin_bit_cast(u32x2, lo)[0];
+      w[1] = __builtin_bit_cast(u32x2, lo)[1];
+      w[2] = __builtin_bit_cast(u32x2, hi)[0];
+      w[3] = __builtin_bit_cast(u32x2, hi)[1];
+      return w;
+    };
+    vf[0] = vread(0);
+    vf[1] = vread(1);
+    float rs0 = Sc[0][0], rs1 = Sc[0][1];
+    float m0 = Sn[0][0];
+#pragma unroll
+    for (int st = 0; st < NB; ++st) {
+      const int t = st / DBLK, db = st % DBLK;
+      if (st + 2 < NB) vf[(st + 2) % 3] = vread(st + 2);
+      oacc[db] = E::mfma32(as_vec8<V8>(vf[st % 3]), pf[t], oacc[db]);
+      if (loads && st % kLoadEvery == kLoadEvery / 2 && st / kLoadEvery < NI)
+        load_one(rs, st / kLoadEvery, ldst);
+#pragma unroll
+      for (int q = 0; q < EB; q += 2) {
+        const int x = st * EB + q;
+        const int h = x >> 4, r = x & 15;
+        if (x > 0) {
+          rs0 += Sc[h][r];
+          rs1 += Sc[h][r + 1];
+        }
+        m0 = (x == 0) ? __builtin_fmaxf(m0, Sn[h][r + 1])
+                      : __builtin_fmaxf(__builtin_fmaxf(m0, Sn[h][r]), Sn[h][r + 1]);
+      }
+      // pin this step's VALU work under this step's MFMA
+      asm volatile("" : "+v"(rs0), "+v"(rs1), "+v"(m0));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_run += rs0 + rs1;
+    mh = m0;
   };
 
-  HCP_LDS(char)* A = (HCP_LDS(char)*)(bufA);
-  HCP_LDS(char)* B = (HCP_LDS(char)*)(bufB);
+  // One iteration n of the software pipeline (S_cur = scores of tile n, masked
+  // and checked against m_ref; S_nxt receives tile n+1): phase A, then the
+  // masking of tile n+1 when it is a diagonal or ragged tile, then phase B,
+  // then the (rare) rescale for tile n+1.  On a wave's last tile phase A
+  // multiplies a stale LDS tile whose result is discarded.  The four tile
+  // buffers are distinct __shared__ objects so the compiler can tell the LDS
+  // reads from the global->LDS writes in flight and does not wait for them.
+  auto iterate = [&](int n, f32x16 (&Sc)[2], f32x16 (&Sn)[2], HCP_LDS(char)* kload,
+                     HCP_LDS(char)* vload, const HCP_LDS(char)* Ks,
+                     const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
+    // loads for the next iteration: K(n+2) -> kload, V(n+1) -> vload.
+    // Contiguous segments issue them one at a time under the MFMAs of phases
+    // A (K) and B (V); paged segments (block-table lookups) issue them here.
+    bool spread = false;
+    const __amdgpu_buffer_rsrc_t rsk = tile_rsrc(kseg, n + 2);  // unused when paged
+    const __amdgpu_buffer_rsrc_t rsv = tile_rsrc(vseg, n + 1);
+    if constexpr (PAGED) {
+      if (n + 2 < ntiles) issue(kseg, n + 2, bid_k, kload);
+      if (n + 1 < ntiles) issue(vseg, n + 1, bid_v, vload);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) bid_v[i] = bid_k[i];
+      if (n + 3 < ntiles) fetch_blocks(n + 3, bid_f);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) bid_k[i] = bid_f[i];
+    } else {
+      spread = n < wtiles;
+      if (!spread) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          load_one(rsk, i, kload);
+          load_one(rsv, i, vload);
+        }
+      }
+    }
+    if (n < wtiles) {
+      phase_a(Ks, Sc, Sn, rsk, kload, spread);
+      if (needs_mask(n + 1)) apply_mask(Sn, n + 1);
+      float mh;
+      phase_b(Vs, Sc, Sn, mh, rsv, vload, spread);
+      if (n + 1 < wtiles) check_rescale(mh);
+    }
+    __syncthreads();  // waits for this iteration's tile loads (vmcnt(0)) first
+  };
 
+  HCP_LDS(char)* K0 = (HCP_LDS(char)*)(bufK0);
+  HCP_LDS(char)* K1 = (HCP_LDS(char)*)(bufK1);
+  HCP_LDS(char)* V0 = (HCP_LDS(char)*)(bufV0);
+  HCP_LDS(char)* V1 = (HCP_LDS(char)*)(bufV1);
+
+  // ---- prologue: K(0), K(1), V(0) in flight; S(0) = K(0) Q^T ----
   if (ntiles > 0) {
-    fetch_blocks(0);
-    issue_tile(0, A);
-    if (ntiles > 1) fetch_blocks(1);
+    fetch_blocks(0, bid_f);
+    issue(kseg, 0, bid_f, K0);
+    issue(vseg, 0, bid_f, V0);
+    if (ntiles > 1) {
+      fetch_blocks(1, bid_v);
+      issue(kseg, 1, bid_v, K1);
+    }
+    if (ntiles > 2) fetch_blocks(2, bid_k);
   }
   __syncthreads();
-  for (int it = 0; it < ntiles; it += 2) {
-    if (it + 1 < ntiles) {
-      issue_tile(it + 1, B);
-      if (it + 2 < ntiles) fetch_blocks(it + 2);
-    }
-    tile_step(A, it * BN);
-    __syncthreads();
-    if (it + 1 >= ntiles) break;
-    if (it + 2 < ntiles) {
-      issue_tile(it + 2, A);
-      if (it + 3 < ntiles) fetch_blocks(it + 3);
-    }
-    tile_step(B, (it + 1) * BN);
-    __syncthreads();
+  if (wtiles > 0) {
+    qk(K0, SA);
+    if (needs_mask(0)) apply_mask(SA, 0);
+    check_rescale(tile_max(SA));
   }
+  __syncthreads();  // K(0) is read by every wave before K(2) overwrites it
+
+  // iteration n reads K(n+1), V(n) and loads K(n+2), V(n+1); buffers by parity
+  int n = 0;
+  for (; n + 1 < ntiles; n += 2) {
+    iterate(n, SA, SB, K0, V1, K1, V0);
+    iterate(n + 1, SB, SA, K1, V0, K0, V1);
+  }
+  if (n < ntiles) iterate(n, SA, SB, K0, V1, K1, V0);
 
   // ---- epilogue ----
   const float l_tot = l_run + __shfl_xor(l_run, 32);
