@@ -183,6 +183,151 @@ def bench_decode(dev, steps, warmup):
     }
 
 
+def timed(fn, steps, warmup):
+    """Mean ms of fn() over `steps` runs after `warmup`, HIP events on the
+    current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+
+
+def bench_varlen(dev, steps, warmup, seed=2, nreq=16, bs=16):
+    """Continuous-batch varlen prefill: 16 requests, local lengths U[512, 4096]
+    causal over a paged [num_blocks, 4, 16, 256] cache (random block table,
+    the row also covers the request's prefix blocks, which are not read),
+    peer prefixes 16*U[64, 1024] packed contiguously.  One launch per segment
+    kind for the whole batch, then one merge over all rows."""
+    from hcp_vllm_plugin_amd import merge_attn_states
+    from hcp_vllm_plugin_amd.varlen import (
+        PagedCache, VarlenLaunch, make_entry, segment_contiguous, segment_paged)
+
+    gen = torch.Generator().manual_seed(seed)
+    loc = torch.randint(512, 4097, (nreq,), generator=gen).tolist()
+    pre = (16 * torch.randint(64, 1025, (nreq,), generator=gen)).tolist()
+    blocks = [-(-(p + l) // bs) for p, l in zip(pre, loc)]
+    nb = sum(blocks) + 8
+    dgen = torch.Generator(device=dev).manual_seed(seed)
+    cache = torch.randn(nb, HKV, bs, 2 * D, generator=dgen, device=dev).to(torch.bfloat16)
+    tq, tp = sum(loc), sum(pre)
+    q = torch.randn(tq, H, D, generator=dgen, device=dev).to(torch.bfloat16)
+    pk = torch.randn(tp, HKV, D, generator=dgen, device=dev).to(torch.bfloat16)
+    pv = torch.randn(tp, HKV, D, generator=dgen, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(nb, generator=gen).to(torch.int32)
+    bt = torch.zeros(nreq, max(blocks), dtype=torch.int32)
+    o = 0
+    for r, nbk in enumerate(blocks):
+        bt[r, :nbk] = perm[o:o + nbk]
+        o += nbk
+    bt = bt.to(dev)
+    pc = PagedCache.from_tensor(cache)
+    loc_e, peer_e = [], []
+    qs = ps = 0
+    for r in range(nreq):
+        loc_e.append(make_entry(qs, loc[r], segment_paged(pc, bt[r], pre[r], loc[r]), 0))
+        peer_e.append(make_entry(qs, loc[r], segment_contiguous(pk, pv, ps, pre[r])))
+        qs += loc[r]
+        ps += pre[r]
+    l_launch = VarlenLaunch(loc_e, True, True, dev)
+    p_launch = VarlenLaunch(peer_e, False, False, dev)
+    o_loc, o_peer, out = (torch.empty_like(q) for _ in range(3))
+    lse_loc = torch.empty(H, tq, device=dev)
+    lse_peer = torch.empty(H, tq, device=dev)
+    t_loc = timed(lambda: l_launch.run(q, o_loc, lse_loc, HKV, SCALE), steps, warmup)
+    t_peer = timed(lambda: p_launch.run(q, o_peer, lse_peer, HKV, SCALE), steps, warmup)
+    t_merge = timed(lambda: merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc),
+                    steps, warmup)
+    pairs_l = sum(causal_pairs(l, l, 0) for l in loc)
+    pairs_p = sum(l * p for l, p in zip(loc, pre))
+    f_l, f_p = 4 * D * H * pairs_l, 4 * D * H * pairs_p
+    t = t_loc + t_peer + t_merge
+    tf = (f_l + f_p) / (t * 1e-3) / 1e12
+    return {
+        "workload": (f"varlen prefill: {nreq} requests, local U[512,4096] causal over a paged "
+                     f"[nb,4,16,256] cache + peer 16*U[64,1024] contiguous, one launch per "
+                     f"segment kind, then the merge"),
+        "query_tokens": tq, "peer_tokens": tp,
+        "ms": round(t, 4), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+        "local_paged": {"ms": round(t_loc, 4),
+                        "tflops": round(f_l / (t_loc * 1e-3) / 1e12, 2)},
+        "peer": {"ms": round(t_peer, 4), "tflops": round(f_p / (t_peer * 1e-3) / 1e12, 2)},
+        "merge_ms": round(t_merge, 4),
+        "tflop": round((f_l + f_p) / 1e12, 3),
+    }
+
+
+def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
+    """Long-context layer at the Llama-3-70B attention shape (64 / 8 heads,
+    head_dim 128), bf16: 65536 local query tokens causal over local keys
+    (global offset 65536: the peer chunk comes first) + 65536 peer keys,
+    processed as 8 query chunks of 8192; chunk c attends local keys
+    [0, 8192(c+1)) at offset 8192c, then all peer keys, then the LSE merge."""
+    from hcp_vllm_plugin_amd import merge_attn_states, ring_attn_with_lse
+
+    h, hkv = 64, 8
+    dgen = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(n, h, D, generator=dgen, device=dev).to(torch.bfloat16)
+    kl = torch.randn(n, hkv, D, generator=dgen, device=dev)
+    kp = torch.randn(n, hkv, D, generator=dgen, device=dev)
+    ch = torch.randperm(D, generator=torch.Generator().manual_seed(seed))[:4].to(dev)
+    kl[..., ch] *= 8.0
+    kp[..., ch] *= 8.0
+    kl, kp = kl.to(torch.bfloat16), kp.to(torch.bfloat16)
+    vl = torch.randn(n, hkv, D, generator=dgen, device=dev).to(torch.bfloat16)
+    vp = torch.randn(n, hkv, D, generator=dgen, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    nchunk = n // chunk
+    t_attn = [0.0]
+    t_merge = [0.0]
+
+    def step(ev=None):
+        for c in range(nchunk):
+            qc = q[c * chunk:(c + 1) * chunk]
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e2 = torch.cuda.Event(enable_timing=True)
+            if ev is not None:
+                e0.record()
+            o_l, l_l = ring_attn_with_lse(qc, kl[:chunk * (c + 1)], vl[:chunk * (c + 1)],
+                                          SCALE, chunk * c)
+            o_p, l_p = ring_attn_with_lse(qc, kp, vp, SCALE, None)
+            if ev is not None:
+                e1.record()
+            merge_attn_states(out[c * chunk:(c + 1) * chunk], o_p, l_p, o_l, l_l)
+            if ev is not None:
+                e2.record()
+                ev.append((e0, e1, e2))
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(evs)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    attn = sum(a.elapsed_time(b) for a, b, _ in evs) / steps
+    merge = sum(b.elapsed_time(c) for _, b, c in evs) / steps
+    pairs = sum(causal_pairs(chunk, chunk * (c + 1), chunk * c) for c in range(nchunk)) + n * n
+    flops = 4 * D * h * pairs
+    tf = flops / (wall * 1e-3) / 1e12
+    return {
+        "workload": ("Llama-3-70B attention shape (64/8 heads, head_dim 128) bf16: 65536 local "
+                     "causal + 65536 peer keys, 8 query chunks of 8192 with the LSE merge"),
+        "ms": round(wall, 3), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+        "attn_ms": round(attn, 3), "merge_ms": round(merge, 3),
+        "merge_overhead": round(merge / wall, 4), "tflop": round(flops / 1e12, 2),
+    }
+
+
 def cpu_baseline(budget_s=30.0):
     """CPU oracle (torch fp32 restatement of the reference's fallback path) on
     the prefill workload itself.
@@ -260,7 +405,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--part", choices=("all", "prefill", "decode", "copy"), default="all",
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the varlen and 70B long-context measurements")
+    ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b", "copy"),
+                    default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -280,11 +428,21 @@ def main():
     if args.part == "decode":
         print(json.dumps(bench_decode(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "varlen":
+        print(json.dumps(bench_varlen(dev, args.steps, args.warmup)), flush=True)
+        return
+    if args.part == "llama70b":
+        print(json.dumps(bench_llama70b(dev, 2, 1)), flush=True)
+        return
     pre = bench_prefill(dev, args.steps, args.warmup)
     if args.part == "prefill":
         print(json.dumps(pre), flush=True)
         return
     dec = None if args.no_decode else bench_decode(dev, args.steps, args.warmup)
+    extra = {}
+    if not args.no_configs:
+        extra["varlen16_paged"] = bench_varlen(dev, args.steps, args.warmup)
+        extra["llama70b_128k"] = bench_llama70b(dev, 2, 1)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 
@@ -351,6 +509,8 @@ def main():
                 "traffic": traffic.get("decode_split", {}).get("bytes"),
             },
         }
+    if extra:
+        line["configs"] = extra
     print(json.dumps(line), flush=True)
 
 

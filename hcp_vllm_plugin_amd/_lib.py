@@ -52,7 +52,7 @@ EXPORTED_SYMBOLS = (
     "hcp_merge_attn_states",
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class KvSegment(ctypes.Structure):
@@ -90,7 +90,7 @@ class DecodeSplit(ctypes.Structure):
         ("entry", ctypes.c_int32),
         ("key_begin", ctypes.c_int32),
         ("key_end", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("slot", ctypes.c_int32),
     ]
 
 

@@ -229,11 +229,17 @@ int hcp_plan_decode_splits(const hcp_varlen_entry* entries, int32_t num_entries,
       splits_out[n].entry = i;
       splits_out[n].key_begin = static_cast<int32_t>(b);
       splits_out[n].key_end = static_cast<int32_t>(std::min<int64_t>(len, b + split_tokens));
-      splits_out[n].reserved = 0;
+      splits_out[n].slot = n;
       ++n;
     }
   }
   while (cur < num_seqs) seq_partial_start[++cur] = n;
+  // dispatch order: longest first, so the last workgroups of the launch are
+  // the short splits and the machine drains evenly
+  std::stable_sort(splits_out, splits_out + n, [](const hcp_decode_split& a,
+                                                  const hcp_decode_split& b) {
+    return a.key_end - a.key_begin > b.key_end - b.key_begin;
+  });
   return n;
 }
 

@@ -58,6 +58,12 @@ namespace hcp {
 #ifndef HCP_MFMA_PRIO
 #define HCP_MFMA_PRIO 3
 #endif
+#ifndef HCP_KPF
+#define HCP_KPF 3  // K fragment reads issued this many MFMAs ahead (phase A)
+#endif
+#ifndef HCP_VPF
+#define HCP_VPF 2  // V fragment reads issued this many MFMAs ahead (phase B)
+#endif
 #ifndef HCP_FWD_WAVES_PER_EU
 #define HCP_FWD_WAVES_PER_EU 2
 #endif
@@ -324,6 +330,7 @@ fa_fwd_kernel(FwdParams p) {
   // tile's scores exceed it by more than kRescaleThresh, so P <= 2^8.
   const float c = p.scale_log2;
   float m_ref = -INFINITY;
+  float thr_raw = -INFINITY;  // (m_ref + threshold) / c: the rescale test on raw scores
   float l_run = 0.f;
   f32x16 oacc[DBLK];
 #pragma unroll
@@ -383,7 +390,7 @@ fa_fwd_kernel(FwdParams p) {
   // than the threshold (a wave vote); the row pair (lane, lane^32) then agrees
   // on the new reference.  O and l hold everything up to the previous tile.
   auto check_rescale = [&](float mh) __attribute__((always_inline)) {
-    if (__any(mh * c > m_ref + kRescaleThresh)) {
+    if (__any(mh > thr_raw)) {
       const float mrow = __builtin_fmaxf(mh, __shfl_xor(mh, 32)) * c;
       const float m_new = __builtin_fmaxf(m_ref, mrow);
       const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
@@ -391,6 +398,8 @@ fa_fwd_kernel(FwdParams p) {
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
       m_ref = m_new;
+      // raw scores above thr_raw would give P > 2^8 against m_ref
+      thr_raw = (m_ref + kRescaleThresh) / c;
     }
   };
 
@@ -468,18 +477,19 @@ fa_fwd_kernel(FwdParams p) {
                      __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads)
       __attribute__((always_inline)) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-    V8 kf[4];
+    constexpr int KR = HCP_KPF + 1;  // K fragment ring
+    V8 kf[KR];
 #pragma unroll
-    for (int j = 0; j < 3; ++j)
+    for (int j = 0; j < HCP_KPF; ++j)
       kf[j] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
 #pragma unroll
     for (int st = 0; st < NA; ++st) {
       const int s = st >> 1, blk = st & 1;
-      if (st + 3 < NA) {
-        const int j = st + 3;
-        kf[j & 3] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
+      if (st + HCP_KPF < NA) {
+        const int j = st + HCP_KPF;
+        kf[j % KR] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
       }
-      Sn[blk] = E::mfma32(kf[st & 3], qf[s], s == 0 ? f32x16{} : Sn[blk]);
+      Sn[blk] = E::mfma32(kf[st % KR], qf[s], s == 0 ? f32x16{} : Sn[blk]);
       if (loads && st % kLoadEvery == kLoadEvery / 2 && st / kLoadEvery < NI)
         load_one(rs, st / kLoadEvery, ldst);
       // scores st*EA .. st*EA+EA-1 of the current tile: half h, regs r..
@@ -511,7 +521,8 @@ fa_fwd_kernel(FwdParams p) {
   auto phase_b = [&](const HCP_LDS(char)* Vs, const f32x16 (&Sc)[2], const f32x16 (&Sn)[2],
                      float& mh, __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads)
       __attribute__((always_inline)) {
-    u32x4 vf[3];
+    constexpr int VR = HCP_VPF + 1;  // V fragment ring
+    u32x4 vf[VR];
     auto vread = [&](int j) __attribute__((always_inline)) {
       const int t = j / DBLK, db = j % DBLK;
       const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
@@ -523,15 +534,15 @@ fa_fwd_kernel(FwdParams p) {
       w[3] = __builtin_bit_cast(u32x2, hi)[1];
       return w;
     };
-    vf[0] = vread(0);
-    vf[1] = vread(1);
+#pragma unroll
+    for (int j = 0; j < HCP_VPF; ++j) vf[j] = vread(j);
     float rs0 = Sc[0][0], rs1 = Sc[0][1];
     float m0 = Sn[0][0];
 #pragma unroll
     for (int st = 0; st < NB; ++st) {
       const int t = st / DBLK, db = st % DBLK;
-      if (st + 2 < NB) vf[(st + 2) % 3] = vread(st + 2);
-      oacc[db] = E::mfma32(as_vec8<V8>(vf[st % 3]), pf[t], oacc[db]);
+      if (st + HCP_VPF < NB) vf[(st + HCP_VPF) % VR] = vread(st + HCP_VPF);
+      oacc[db] = E::mfma32(as_vec8<V8>(vf[st % VR]), pf[t], oacc[db]);
       if (loads && st % kLoadEvery == kLoadEvery / 2 && st / kLoadEvery < NI)
         load_one(rs, st / kLoadEvery, ldst);
 #pragma unroll

@@ -97,6 +97,7 @@ __device__ __forceinline__ u32x2 ldg8(const void* p) {
   return *reinterpret_cast<gu32x2*>(reinterpret_cast<uintptr_t>(p));
 }
 
+
 __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);  // v_exp_f32; exp2(-inf) = 0
 }

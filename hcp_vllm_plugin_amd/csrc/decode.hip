@@ -13,7 +13,9 @@
 //    own 32-key chunks straight from global memory into MFMA operands (no LDS,
 //    no barrier in the loop); the next chunk's loads are in flight while the
 //    current one is computed.
-//      S^T = K Q^T   A = K rows (one key per lane row), B = Q^T
+//      S^T = K Q^T   A = K rows (one key per lane row), B = Q^T; k-step s
+//                    covers d = 32s .. 32s+31, so each K load instruction
+//                    reads one contiguous 64 B piece of 16 key rows
 //      O^T = V^T P^T A = V^T, B = P^T taken from the S^T registers.
 //    For V^T each lane loads 8 keys x 8 contiguous d (16 B per key, whole
 //    256 B rows per load instruction) and transposes the 8x8 block in
@@ -38,7 +40,6 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
   using E = Elem<T>;
   using V8 = typename E::vec8;
   constexpr int QSTEPS = D / 32;  // 16x16x32 k-steps over d
-  constexpr int DW = D / 4;       // d values per lane group in QK
   constexpr int NU = D / 16;      // PV MFMAs (d = NU*row + u)
   static_assert(D == 64 || D == 128, "head_dim");
 
@@ -65,7 +66,7 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
                         static_cast<int64_t>(kvh * G + (hv ? c16 : 0)) * p.q_stride_head) * 2;
 #pragma unroll
     for (int s = 0; s < QSTEPS; ++s) {
-      u32x4 x = hv ? ldg16(qrow + (DW * g4 + 8 * s) * 2) : u32x4{0, 0, 0, 0};
+      u32x4 x = hv ? ldg16(qrow + (32 * s + 8 * g4) * 2) : u32x4{0, 0, 0, 0};
       qf[s] = as_vec8<V8>(x);
     }
   }
@@ -84,9 +85,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
     for (int b = 0; b < 2; ++b) {
       const int64_t key = k0 + 16 * b + c16;
       if (key < ke) {
-        const char* src = kva.k + (kva.offset<PAGED>(key, kvh) + DW * g4) * 2;
+        const char* src = kva.k + (kva.offset<PAGED>(key, kvh) + 8 * g4) * 2;
 #pragma unroll
-        for (int s = 0; s < QSTEPS; ++s) kreg[b][s] = ldg16(src + 16 * s);
+        for (int s = 0; s < QSTEPS; ++s) kreg[b][s] = ldg16(src + 64 * s);
       } else {
 #pragma unroll
         for (int s = 0; s < QSTEPS; ++s) kreg[b][s] = u32x4{0, 0, 0, 0};
@@ -222,8 +223,8 @@ decode_split_kernel(DecParams p) {
   int kvh;
   int64_t item;
   if (!xcd_remap(blockIdx.x, p.num_splits, p.num_kv_heads, &kvh, &item)) return;
-  const int sp = static_cast<int>(item);
-  const hcp_decode_split spl = p.splits[sp];
+  const hcp_decode_split spl = p.splits[item];
+  const int sp = spl.slot;  // workspace partial of this split
   const hcp_varlen_entry e = p.entries[spl.entry];
   if (e.kv.block_table != 0)
     decode_split_body<D, T, true>(p, kvh, sp, e, spl);

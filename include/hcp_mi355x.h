@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 1
+#define HCP_ABI_VERSION 2
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -90,12 +90,18 @@ typedef struct hcp_varlen_entry {
   hcp_kv_segment kv;
 } hcp_varlen_entry;
 
-/* One decode work split: keys [key_begin, key_end) of entry `entry`. */
+/*
+ * One decode work split: keys [key_begin, key_end) of entry `entry`.  Its
+ * fp32 partial goes to workspace slot `slot`; the slots of sequence s are
+ * seq_partial_start[s] .. seq_partial_start[s+1]-1, each used by exactly one
+ * split.  Splits run in array order, so the array order is the dispatch
+ * order and need not follow the slots.
+ */
 typedef struct hcp_decode_split {
   int32_t entry;
   int32_t key_begin;
   int32_t key_end;
-  int32_t reserved;
+  int32_t slot;
 } hcp_decode_split;
 
 int hcp_abi_version(void);
@@ -160,10 +166,12 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok,
  * Host-side split planner for hcp_decode_splitkv.  Each entry is one query
  * token (q_len == 1) of sequence entry_seq[e]; entries of one sequence must be
  * adjacent.  Splits every entry's visible key range into pieces of at most
- * `split_tokens` keys, in sequence order, writing `splits_out` (host) and
+ * `split_tokens` keys, writing `splits_out` (host) and
  * seq_partial_start[num_seqs + 1] (host): the partial slots of sequence s are
- * [seq_partial_start[s], seq_partial_start[s+1]).  Returns the number of
- * splits (or a negative status).  A causal entry sees keys j <= causal_offset.
+ * [seq_partial_start[s], seq_partial_start[s+1]), numbered in sequence order.
+ * The splits are listed longest first (ties in sequence order), so the short
+ * ones fill the end of the launch.  Returns the number of splits (or a
+ * negative status).  A causal entry sees keys j <= causal_offset.
  */
 int hcp_plan_decode_splits(const hcp_varlen_entry* entries,
                            int32_t num_entries, const int32_t* entry_seq,

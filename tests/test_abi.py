@@ -135,11 +135,20 @@ def test_plan_decode_splits_partition_each_segment(L):
                 assert 0 < k - b <= split
                 keys.extend(range(b, k))
         assert keys == list(range(e.kv.len))
-    # partial slots of sequence s are exactly the splits of its entries
+    # partial slots of sequence s are exactly the splits of its entries, and
+    # the slots are a permutation of 0..n-1
+    slots = [out[i].slot for i in range(n)]
+    assert sorted(slots) == list(range(n))
     for s in range(len(seqs)):
-        mine = [i for i, (en, _, _) in enumerate(sp) if seq_of[en] == s]
+        mine = sorted(slots[i] for i, (en, _, _) in enumerate(sp) if seq_of[en] == s)
         assert mine == list(range(starts[s], starts[s + 1]))
     assert starts[len(seqs)] == n
+    # dispatch order: longest first; equal lengths keep sequence order
+    lens = [k - b for _, b, k in sp]
+    assert lens == sorted(lens, reverse=True)
+    for i in range(n - 1):
+        if lens[i] == lens[i + 1]:
+            assert slots[i] < slots[i + 1]
 
 
 def test_plan_decode_splits_causal_limit_and_errors(L):
