@@ -224,11 +224,14 @@ int hcp_plan_decode_splits(const hcp_varlen_entry* entries, int32_t num_entries,
     while (cur < s) seq_partial_start[++cur] = n;
     int64_t len = entries[i].kv.len;
     if (causal) len = std::max<int64_t>(0, std::min<int64_t>(len, entries[i].causal_offset + 1));
-    for (int64_t b = 0; b < len; b += split_tokens) {
+    // ceil(len / split_tokens) pieces of (nearly) equal size
+    const int64_t pieces = (len + split_tokens - 1) / split_tokens;
+    const int64_t step = pieces > 0 ? (len + pieces - 1) / pieces : 0;
+    for (int64_t b = 0; b < len; b += step) {
       if (n >= cap || !splits_out) return fail(HCP_EWORKSPACE, "%s: split cap %d exceeded", who, cap);
       splits_out[n].entry = i;
       splits_out[n].key_begin = static_cast<int32_t>(b);
-      splits_out[n].key_end = static_cast<int32_t>(std::min<int64_t>(len, b + split_tokens));
+      splits_out[n].key_end = static_cast<int32_t>(std::min<int64_t>(len, b + step));
       splits_out[n].slot = n;
       ++n;
     }

@@ -32,24 +32,52 @@ namespace hcp {
 
 constexpr int kDecThreads = 256;
 constexpr int kDecChunk = 32;  // keys per wave step
+// raw buffer descriptor word 3 (32-bit data format, bounds-checked)
+constexpr int kBufWord3 = 0x00020000;
+// cache policy of the K/V stream: non-temporal (read once per launch)
+constexpr int kStreamAux = 2;
+#define HCP_LDS_PTR(T) __attribute__((address_space(3))) T*
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt
+// and lgkmcnt left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS of the split kernel, shared by its paged and contiguous instantiations.
+template <int D>
+struct DecShared {
+  static constexpr int CHB = kDecChunk * D * 2;  // bytes of a chunk's K (or V) rows
+};
 
 template <int D, typename T, bool PAGED>
 __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, int sp,
                                                   const hcp_varlen_entry& e,
-                                                  const hcp_decode_split& spl) {
+                                                  const hcp_decode_split& spl,
+                                                  char (*bufE)[2 * DecShared<D>::CHB],
+                                                  char (*bufO)[2 * DecShared<D>::CHB],
+                                                  float (*sm_m)[16], float (*sm_l)[16]) {
   using E = Elem<T>;
   using V8 = typename E::vec8;
-  constexpr int QSTEPS = D / 32;  // 16x16x32 k-steps over d
-  constexpr int NU = D / 16;      // PV MFMAs (d = NU*row + u)
+  constexpr int QSTEPS = D / 32;         // 16x16x32 k-steps over d
+  constexpr int NU = D / 16;             // PV MFMAs (d = NU*row + u)
+  constexpr int ROWB = D * 2;            // bytes of one key row of one head
+  constexpr int CPR = ROWB / 16;         // 16-byte slots per row
+  constexpr int CHB = kDecChunk * ROWB;  // bytes of the K (or V) rows of a chunk
+  constexpr int NLD = CHB / 1024;        // LDS-DMA instructions per K (or V) chunk
+  constexpr int KPI = 1024 / ROWB;       // key rows per DMA instruction
   static_assert(D == 64 || D == 128, "head_dim");
 
-  __shared__ float sm_m[4][16];
-  __shared__ float sm_l[4][16];
-  __shared__ float sm_o[4][16][D];
+  // Wave-private chunk buffers [K rows | V rows] (bufE / bufO: even / odd
+  // chunks of the wave, distinct objects so the compiler can tell reads of
+  // one from the DMA writes into the other).  Row r's 16-byte slot c sits at
+  // slot c ^ (r % CPR): both operand reads below are then conflict-free.
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
   const int G = p.group;
@@ -57,7 +85,8 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
   kva.init(e.kv);
   const int64_t kb = spl.key_begin, ke = spl.key_end;
 
-  // Q^T (B operand): column c16 = query head kvh*G + c16 (zero for c16 >= G)
+  // Q^T (B operand): column c16 = query head kvh*G + c16 (zero for c16 >= G);
+  // k-step s covers d = 32s .. 32s+31 (lane group g4: 8 of them)
   V8 qf[QSTEPS];
   {
     const bool hv = c16 < G;
@@ -77,61 +106,82 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
 #pragma unroll
   for (int u = 0; u < NU; ++u) oacc[u] = f32x4{};
 
-  // chunk registers: K rows (2 blocks of 16 keys) and V rows (8 keys)
-  u32x4 kreg[2][QSTEPS];
-  u32x4 vreg[8];  // D=128: 8 d per key; D=64 uses the low half
-  auto load_chunk = [&](int64_t k0) {
+  // ---- HBM -> LDS: one chunk (32 keys) of K and V rows ----
+  // DMA instruction j writes rows j*KPI .. j*KPI+KPI-1; lane -> (row kr, slot
+  // sl), fetching the row's 16-byte piece (sl ^ row % CPR): every
+  // instruction reads KPI whole rows (1 KB), streamed past the caches.
+  const int kr = lane / CPR, sl = lane % CPR;
+  const int64_t rowb_g = kva.stride_tok * 2;
+  auto issue = [&](int64_t k0, HCP_LDS_PTR(char) dst) __attribute__((always_inline)) {
+    if constexpr (!PAGED) {
+      const int64_t rows = ke - k0;  // >= 1 valid rows in this chunk
+      const int nrec = rows >= kDecChunk ? 0x7fffffff
+                                         : static_cast<int>((rows - 1) * rowb_g) + ROWB;
+      const int64_t base = ((kva.start + k0) * kva.stride_tok +
+                            static_cast<int64_t>(kvh) * kva.stride_head) * 2;
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kva.k + base), 0, nrec, kBufWord3);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kva.v + base), 0, nrec, kBufWord3);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int64_t key = k0 + 16 * b + c16;
-      if (key < ke) {
-        const char* src = kva.k + (kva.offset<PAGED>(key, kvh) + 8 * g4) * 2;
-#pragma unroll
-        for (int s = 0; s < QSTEPS; ++s) kreg[b][s] = ldg16(src + 64 * s);
-      } else {
-#pragma unroll
-        for (int s = 0; s < QSTEPS; ++s) kreg[b][s] = u32x4{0, 0, 0, 0};
+      for (int j = 0; j < NLD; ++j) {
+        const int row = j * KPI + kr;
+        const int off = static_cast<int>(row * rowb_g) + 16 * (sl ^ (row % CPR));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, reinterpret_cast<HCP_LDS_PTR(void)>(dst + j * 1024), 16, off, 0, 0, kStreamAux);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16, off, 0, 0,
+            kStreamAux);
       }
-    }
+    } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t key = k0 + 16 * (j >> 2) + 4 * g4 + (j & 3);
-      if (key < ke) {
-        const char* src = kva.v + (kva.offset<PAGED>(key, kvh) + NU * c16) * 2;
-        if constexpr (NU == 8) {
-          vreg[j] = ldg16(src);
-        } else {
-          u32x2 x = ldg8(src);
-          vreg[j] = u32x4{x[0], x[1], 0, 0};
-        }
-      } else {
-        vreg[j] = u32x4{0, 0, 0, 0};
+      for (int j = 0; j < NLD; ++j) {
+        const int row = j * KPI + kr;
+        int64_t key = k0 + row;
+        key = key < ke ? key : ke - 1;  // rows past the split: masked below
+        const int64_t o = (kva.offset<true>(key, kvh) + 8 * (sl ^ (row % CPR))) * 2;
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const __attribute__((address_space(1))) void*>(
+                reinterpret_cast<uintptr_t>(kva.k + o)),
+            reinterpret_cast<HCP_LDS_PTR(void)>(dst + j * 1024), 16, 0, kStreamAux);
+        __builtin_amdgcn_global_load_lds(
+            reinterpret_cast<const __attribute__((address_space(1))) void*>(
+                reinterpret_cast<uintptr_t>(kva.v + o)),
+            reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16, 0, kStreamAux);
       }
     }
   };
 
-  const int64_t nchunks = (ke - kb + kDecChunk - 1) / kDecChunk;
-  int64_t ci = wave;
-  if (ci < nchunks) load_chunk(kb + ci * kDecChunk);
-  while (ci < nchunks) {
-    const int64_t k0 = kb + ci * kDecChunk;
-    // take this chunk's registers, start the next chunk's loads
-    u32x4 kc[2][QSTEPS];
-    u32x4 vc[8];
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int s = 0; s < QSTEPS; ++s) kc[b][s] = kreg[b][s];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) vc[j] = vreg[j];
-    const int64_t cn = ci + 4;
-    if (cn < nchunks) load_chunk(kb + cn * kDecChunk);
-
+  // ---- one chunk from LDS: S^T = K Q^T, online softmax, O^T += V^T P^T ----
+  auto compute = [&](int64_t k0, const HCP_LDS_PTR(char) src) __attribute__((always_inline)) {
+    // K rows 16b + c16, d = 32s + 8g4 .. +7: slot (4s + g4) of that row
     f32x4 s0 = f32x4{}, s1 = f32x4{};
 #pragma unroll
     for (int s = 0; s < QSTEPS; ++s) {
-      s0 = E::mfma16(as_vec8<V8>(kc[0][s]), qf[s], s0);
-      s1 = E::mfma16(as_vec8<V8>(kc[1][s]), qf[s], s1);
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int row = 16 * b + c16;
+        const u32x4 kx = *reinterpret_cast<const HCP_LDS_PTR(u32x4)>(
+            src + row * ROWB + 16 * ((4 * s + g4) ^ (row % CPR)));
+        if (b == 0)
+          s0 = E::mfma16(as_vec8<V8>(kx), qf[s], s0);
+        else
+          s1 = E::mfma16(as_vec8<V8>(kx), qf[s], s1);
+      }
+    }
+    // V rows 16(j>>2) + 4g4 + (j&3), d = NU*c16 .. +NU-1
+    u32x4 vc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 16 * (j >> 2) + 4 * g4 + (j & 3);
+      const HCP_LDS_PTR(char) vrow = src + CHB + row * ROWB;
+      if constexpr (NU == 8) {
+        vc[j] = *reinterpret_cast<const HCP_LDS_PTR(u32x4)>(vrow + 16 * (c16 ^ (row % CPR)));
+      } else {
+        const u32x2 x = *reinterpret_cast<const HCP_LDS_PTR(u32x2)>(
+            vrow + 16 * ((c16 >> 1) ^ (row % CPR)) + 8 * (c16 & 1));
+        vc[j] = u32x4{x[0], x[1], 0, 0};
+      }
     }
     if (k0 + kDecChunk > ke) {
 #pragma unroll
@@ -178,10 +228,43 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
       }
       oacc[u] = E::mfma16(as_vec8<V8>(a), pf, oacc[u]);
     }
-    ci = cn;
+  };
+
+  // ---- the wave's chunks wave, wave+4, ...; next chunk's DMA in flight ----
+  const int64_t nchunks = (ke - kb + kDecChunk - 1) / kDecChunk;
+  HCP_LDS_PTR(char) be = (HCP_LDS_PTR(char))(bufE[wave]);
+  HCP_LDS_PTR(char) bo = (HCP_LDS_PTR(char))(bufO[wave]);
+  // The next chunk's DMA is issued unconditionally (past the wave's last
+  // chunk it re-reads the split's last chunk into the buffer nobody reads):
+  // with no branch around it, the wait before each compute is exactly "the
+  // previous chunk's loads", not a conservative wait for all of them.
+  const int64_t last = nchunks - 1;
+  auto next_k0 = [&](int64_t cn) __attribute__((always_inline)) {
+    return kb + (cn < last ? cn : last) * kDecChunk;
+  };
+  // Before a compute, the wave waits until only the 2*NLD loads it just
+  // issued (into the other buffer) are outstanding: its own DMA into the
+  // buffer it reads has landed.  Buffers are wave-private, so no barrier.
+  int64_t ci = wave;
+  if (ci < nchunks) {
+    issue(kb + ci * kDecChunk, be);
+    while (true) {
+      issue(next_k0(ci + 4), bo);
+      wait_vmcnt<2 * NLD>();
+      compute(kb + ci * kDecChunk, be);
+      ci += 4;
+      if (ci >= nchunks) break;
+      issue(next_k0(ci + 4), be);
+      wait_vmcnt<2 * NLD>();
+      compute(kb + ci * kDecChunk, bo);
+      ci += 4;
+      if (ci >= nchunks) break;
+    }
   }
 
-  // ---- combine the 4 waves ----
+  // ---- combine the 4 waves (the chunk buffers are reused for O) ----
+  __syncthreads();
+  float (*sm_o)[16][D] = reinterpret_cast<float (*)[16][D]>(&bufE[0][0]);
   float l_tot = l_run + __shfl_xor(l_run, 16);
   l_tot += __shfl_xor(l_tot, 32);
   if (g4 == 0) {
@@ -218,8 +301,13 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
 // contiguous, its local segment paged), uniform within a workgroup.
 template <int D, typename T>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
-                          amdgpu_waves_per_eu(2, 2))) void
+                          amdgpu_waves_per_eu(1, 1))) void
 decode_split_kernel(DecParams p) {
+  constexpr int CHB = DecShared<D>::CHB;
+  __shared__ __attribute__((aligned(1024))) char bufE[4][2 * CHB];
+  __shared__ __attribute__((aligned(1024))) char bufO[4][2 * CHB];
+  __shared__ float sm_m[4][16];
+  __shared__ float sm_l[4][16];
   int kvh;
   int64_t item;
   if (!xcd_remap(blockIdx.x, p.num_splits, p.num_kv_heads, &kvh, &item)) return;
@@ -227,9 +315,9 @@ decode_split_kernel(DecParams p) {
   const int sp = spl.slot;  // workspace partial of this split
   const hcp_varlen_entry e = p.entries[spl.entry];
   if (e.kv.block_table != 0)
-    decode_split_body<D, T, true>(p, kvh, sp, e, spl);
+    decode_split_body<D, T, true>(p, kvh, sp, e, spl, bufE, bufO, sm_m, sm_l);
   else
-    decode_split_body<D, T, false>(p, kvh, sp, e, spl);
+    decode_split_body<D, T, false>(p, kvh, sp, e, spl, bufE, bufO, sm_m, sm_l);
 }
 
 template <int D, typename T>

@@ -244,14 +244,15 @@ def varlen_attn_with_lse(
 
 
 def choose_split_tokens(seg_lens: list[int], num_kv_heads: int,
-                        target_workgroups: int = 2048, minimum: int = 256,
-                        maximum: int = 8192) -> int:
+                        target_workgroups: int = 1024, minimum: int = 256,
+                        maximum: int = 16384) -> int:
     """Split size from the batch's total key count.
 
-    Aims at ``target_workgroups`` (split, KV head) workgroups -- 8 per CU on
-    256 CUs -- so every CU streams K/V with several waves in flight, while
-    each split stays long enough that its fp32 partial is small next to the
-    K/V it summarises.  Rounded to 64 keys.
+    Aims at ``target_workgroups`` (split, KV head) workgroups -- 4 per CU on
+    256 CUs, one resident at a time (the split kernel's chunk buffers take
+    128 KB of LDS) -- so the launch drains evenly while each split stays
+    long enough that its fp32 partial is small next to the K/V it
+    summarises.  Rounded to 64 keys.
     """
     total = sum(seg_lens) * num_kv_heads
     if total == 0:

@@ -165,8 +165,9 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok,
 /*
  * Host-side split planner for hcp_decode_splitkv.  Each entry is one query
  * token (q_len == 1) of sequence entry_seq[e]; entries of one sequence must be
- * adjacent.  Splits every entry's visible key range into pieces of at most
- * `split_tokens` keys, writing `splits_out` (host) and
+ * adjacent.  Splits every entry's visible key range into ceil(len /
+ * split_tokens) pieces of nearly equal size (each at most `split_tokens`
+ * keys), writing `splits_out` (host) and
  * seq_partial_start[num_seqs + 1] (host): the partial slots of sequence s are
  * [seq_partial_start[s], seq_partial_start[s+1]), numbered in sequence order.
  * The splits are listed longest first (ties in sequence order), so the short
