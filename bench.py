@@ -263,6 +263,31 @@ def bench_varlen(dev, steps, warmup, seed=2, nreq=16, bs=16):
     }
 
 
+def bench_kv_cache_write(dev, steps, warmup, seed=2, n=43125, nb=12000, bs=16):
+    """Paged KV-cache write (the step before the path): n tokens' K/V [n, 4, 128]
+    bf16 into a [nb, 4, 16, 256] cache at a seeded random slot permutation
+    (n = the varlen batch's new tokens), and the 64-token decode-step write."""
+    from hcp_vllm_plugin_amd.kv_cache import reshape_and_cache
+
+    gen = torch.Generator().manual_seed(seed)
+    dgen = torch.Generator(device=dev).manual_seed(seed)
+    cache = torch.zeros(nb, HKV, bs, 2 * D, dtype=torch.bfloat16, device=dev)
+    key = torch.randn(n, HKV, D, generator=dgen, device=dev).to(torch.bfloat16)
+    value = torch.randn(n, HKV, D, generator=dgen, device=dev).to(torch.bfloat16)
+    slots = torch.randperm(nb * bs, generator=gen)[:n].to(dev)
+    ms = timed(lambda: reshape_and_cache(key, value, cache, slots), steps, warmup)
+    ms64 = timed(lambda: reshape_and_cache(key[:64], value[:64], cache, slots[:64]),
+                 steps, warmup)
+    byts = n * HKV * D * 2 * 2 * 2  # K and V, read and written
+    return {
+        "workload": (f"paged KV-cache write: {n} tokens [n,4,128] bf16 into [nb,4,16,256] at "
+                     f"random slots; and a 64-token decode step"),
+        "ms": round(ms, 4), "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "bytes": byts, "decode_step_us": round(ms64 * 1e3, 2),
+    }
+
+
 def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
     """Long-context layer at the Llama-3-70B attention shape (64 / 8 heads,
     head_dim 128), bf16: 65536 local query tokens causal over local keys
@@ -407,7 +432,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the varlen and 70B long-context measurements")
-    ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b", "copy"),
+    ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
+                                       "kvwrite", "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -431,6 +457,9 @@ def main():
     if args.part == "varlen":
         print(json.dumps(bench_varlen(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "kvwrite":
+        print(json.dumps(bench_kv_cache_write(dev, args.steps, args.warmup)), flush=True)
+        return
     if args.part == "llama70b":
         print(json.dumps(bench_llama70b(dev, 2, 1)), flush=True)
         return
@@ -443,6 +472,7 @@ def main():
     if not args.no_configs:
         extra["varlen16_paged"] = bench_varlen(dev, args.steps, args.warmup)
         extra["llama70b_128k"] = bench_llama70b(dev, 2, 1)
+        extra["kv_cache_write"] = bench_kv_cache_write(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 

@@ -30,6 +30,8 @@ HCP_EWORKSPACE = -4
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
 DTYPE_F32 = 2
+DTYPE_I32 = 3
+DTYPE_I64 = 4
 
 _STATUS_NAMES = {
     HCP_EINVAL: "EINVAL",
@@ -50,9 +52,10 @@ EXPORTED_SYMBOLS = (
     "hcp_decode_workspace_bytes",
     "hcp_decode_splitkv",
     "hcp_merge_attn_states",
+    "hcp_reshape_and_cache",
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class KvSegment(ctypes.Structure):
@@ -80,6 +83,21 @@ class VarlenEntry(ctypes.Structure):
         ("q_len", ctypes.c_int64),
         ("causal_offset", ctypes.c_int64),
         ("kv", KvSegment),
+    ]
+
+
+class PagedCacheDesc(ctypes.Structure):
+    """``hcp_paged_cache`` (include/hcp_mi355x.h)."""
+
+    _fields_ = [
+        ("k_addr", ctypes.c_uint64),
+        ("v_addr", ctypes.c_uint64),
+        ("stride_block", ctypes.c_int64),
+        ("stride_head", ctypes.c_int64),
+        ("stride_tok", ctypes.c_int64),
+        ("num_blocks", ctypes.c_int64),
+        ("block_size", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -131,6 +149,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_decode_splitkv.argtypes = [
         _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I32, _P, ctypes.c_size_t,
         _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _F, _I32, _P,
+    ]
+    lib.hcp_reshape_and_cache.restype = ctypes.c_int
+    lib.hcp_reshape_and_cache.argtypes = [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I64, _I32, _I32, _P, _I32, _P,
     ]
     lib.hcp_merge_attn_states.restype = ctypes.c_int
     lib.hcp_merge_attn_states.argtypes = [

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 OUT = os.path.join(HERE, "libhcp_mi355x.so")
 
-SOURCES = ["abi.hip", "attn_fwd.hip", "decode.hip", "merge.hip"]
+SOURCES = ["abi.hip", "attn_fwd.hip", "decode.hip", "merge.hip", "cache.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -363,4 +363,57 @@ int hcp_merge_attn_states(void* out, int64_t o_stride_tok, int64_t o_stride_head
   return launch_status(hcp::launch_merge(p, static_cast<hipStream_t>(stream)), who);
 }
 
+int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok, int64_t k_stride_head,
+                          const void* value, int64_t v_stride_tok, int64_t v_stride_head,
+                          const void* slot_mapping, int32_t slot_dtype, int64_t num_tokens,
+                          int32_t num_kv_heads, int32_t head_dim, const hcp_paged_cache* cache,
+                          int32_t dtype, void* stream) {
+  const char* who = "hcp_reshape_and_cache";
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return fail(HCP_EINVAL, "%s: bad sizes", who);
+  if (head_dim % 8 || (head_dim & (head_dim - 1)))
+    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d must be a power of two >= 8", who, head_dim);
+  if (!dtype16(dtype)) return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
+  if (slot_dtype != HCP_DTYPE_I32 && slot_dtype != HCP_DTYPE_I64)
+    return fail(HCP_EUNSUPPORTED, "%s: slot dtype %d (int32 or int64)", who, slot_dtype);
+  if (!cache) return fail(HCP_EINVAL, "%s: null cache descriptor", who);
+  const hcp_paged_cache& c = *cache;
+  if (c.block_size <= 0 || (c.block_size & (c.block_size - 1)))
+    return fail(HCP_EINVAL, "%s: block_size %d not a power of two", who, c.block_size);
+  if (c.num_blocks < 0) return fail(HCP_EINVAL, "%s: negative num_blocks", who);
+  if (num_tokens == 0 || c.num_blocks == 0) return HCP_OK;
+  if (!key || !value || !slot_mapping || !c.k_addr || !c.v_addr)
+    return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (!aligned16(key) || !aligned16(value) || (c.k_addr & 15) || (c.v_addr & 15))
+    return fail(HCP_EINVAL, "%s: key/value/cache must be 16-byte aligned", who);
+  if ((k_stride_tok | k_stride_head | v_stride_tok | v_stride_head | c.stride_block |
+       c.stride_head | c.stride_tok) % 8)
+    return fail(HCP_EINVAL, "%s: strides must be multiples of 8 elements", who);
+  if (num_tokens * num_kv_heads > (int64_t)INT32_MAX * 16)
+    return fail(HCP_EINVAL, "%s: too many rows", who);
+  hcp::CacheParams p{};
+  p.key = key;
+  p.k_stride_tok = k_stride_tok;
+  p.k_stride_head = k_stride_head;
+  p.value = value;
+  p.v_stride_tok = v_stride_tok;
+  p.v_stride_head = v_stride_head;
+  p.slots = slot_mapping;
+  p.num_tokens = num_tokens;
+  p.num_kv_heads = num_kv_heads;
+  p.cpr_shift = 31 - __builtin_clz(static_cast<unsigned>(head_dim / 8));
+  p.k_cache = reinterpret_cast<void*>(c.k_addr);
+  p.v_cache = reinterpret_cast<void*>(c.v_addr);
+  p.stride_block = c.stride_block;
+  p.stride_head = c.stride_head;
+  p.stride_tok = c.stride_tok;
+  p.num_slots = c.num_blocks * c.block_size;
+  p.bs_shift = 31 - __builtin_clz(static_cast<unsigned>(c.block_size));
+  p.bs_mask = c.block_size - 1;
+  (void)dtype;  // a 16-bit copy: the bytes are moved as they are
+  return launch_status(hcp::launch_cache_write(p, slot_dtype == HCP_DTYPE_I64,
+                                               static_cast<hipStream_t>(stream)),
+                       who);
+}
+
 }  // extern "C"

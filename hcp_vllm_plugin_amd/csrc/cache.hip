@@ -1,0 +1,57 @@
+// Paged KV-cache write for gfx950: the step right before the attention path.
+//
+// Writes this step's K/V rows [n, Hkv, D] into the paged cache at
+// slot_mapping (slot = block * block_size + offset), the operation of the
+// reference's do_kv_cache_update (hcp_vllm_plugin/ring_backend.py:501-539,
+// torch advanced-index assignment into [nb, 2, bs, Hkv, D]) and of vLLM's
+// reshape_and_cache for the [nb, Hkv, bs, 2*D] layout the local-segment
+// reader consumes (file_connector.py:13-16,175-179).  Both layouts are one
+// stride triple plus separate K and V base addresses.  A negative slot is a
+// padding token and is skipped (vLLM's convention); a slot past the cache is
+// skipped as well, so a bad mapping cannot write outside the cache.
+//
+// HBM-bound copy: each thread moves 16 bytes (8 elements) of one (token,
+// head) row of K and of V, so a wave covers whole 256-byte rows (D = 128) on
+// both sides: 2 * n * Hkv * D * 2 bytes read and the same written.
+#include "params.h"
+
+namespace hcp {
+
+template <typename SlotT>
+__global__ __launch_bounds__(256) void reshape_and_cache_kernel(CacheParams p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t row = gid >> p.cpr_shift;  // (token, head) row
+  if (row >= p.num_tokens * p.num_kv_heads) return;
+  const int ch = static_cast<int>(gid & ((1 << p.cpr_shift) - 1));
+  const int64_t t = row / p.num_kv_heads;
+  const int h = static_cast<int>(row - t * p.num_kv_heads);
+  const int64_t slot = static_cast<int64_t>(reinterpret_cast<const SlotT*>(p.slots)[t]);
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int64_t blk = slot >> p.bs_shift;
+  const int64_t off = slot & p.bs_mask;
+  const int64_t dst = (blk * p.stride_block + static_cast<int64_t>(h) * p.stride_head +
+                       off * p.stride_tok + ch * 8) * 2;
+  const char* k = reinterpret_cast<const char*>(p.key) +
+                  (t * p.k_stride_tok + static_cast<int64_t>(h) * p.k_stride_head + ch * 8) * 2;
+  const char* v = reinterpret_cast<const char*>(p.value) +
+                  (t * p.v_stride_tok + static_cast<int64_t>(h) * p.v_stride_head + ch * 8) * 2;
+  const u32x4 kx = ldg16(k);
+  const u32x4 vx = ldg16(v);
+  *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(p.k_cache) + dst) = kx;
+  *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(p.v_cache) + dst) = vx;
+}
+
+hipError_t launch_cache_write(const CacheParams& p, bool slots_i64, hipStream_t st) {
+  const int64_t threads = (p.num_tokens * p.num_kv_heads) << p.cpr_shift;
+  const int64_t grid = (threads + 255) / 256;
+  if (grid <= 0) return hipSuccess;
+  if (slots_i64)
+    hipLaunchKernelGGL(reshape_and_cache_kernel<int64_t>, dim3(static_cast<unsigned>(grid)),
+                       dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(reshape_and_cache_kernel<int32_t>, dim3(static_cast<unsigned>(grid)),
+                       dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace hcp

@@ -67,10 +67,27 @@ struct MergeParams {
   int32_t out_dtype, p_dtype, s_dtype;
 };
 
+struct CacheParams {
+  const void* key;
+  int64_t k_stride_tok, k_stride_head;
+  const void* value;
+  int64_t v_stride_tok, v_stride_head;
+  const void* slots;  // int32 or int64, one per token
+  int64_t num_tokens;
+  int32_t num_kv_heads;
+  int32_t cpr_shift;  // log2(head_dim / 8): 16-byte chunks per row
+  void* k_cache;
+  void* v_cache;
+  int64_t stride_block, stride_head, stride_tok;
+  int64_t num_slots;  // num_blocks * block_size
+  int32_t bs_shift, bs_mask;
+};
+
 hipError_t launch_fwd(const FwdParams& p, int head_dim, int dtype, bool causal,
                       bool paged, bool varlen, hipStream_t st);
 hipError_t launch_decode(const DecParams& dp, const RedParams& rp, int head_dim,
                          int dtype, hipStream_t st);
 hipError_t launch_merge(const MergeParams& p, hipStream_t st);
+hipError_t launch_cache_write(const CacheParams& p, bool slots_i64, hipStream_t st);
 
 }  // namespace hcp

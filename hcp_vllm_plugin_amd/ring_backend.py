@@ -41,6 +41,7 @@ import os
 import torch
 
 from . import _lib
+from .kv_cache import reshape_and_cache
 from .merge import merge_attn_states
 from .ring_attn import ring_attn_with_lse
 from .varlen import (
@@ -296,22 +297,12 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         """Write this step's K/V into the paged cache at ``slot_mapping``.
 
         ring_backend.py:501-539 (without the decode-ring skip, whose ring
-        transport is not part of this build).  slot = block * bs + offset.
+        transport is not part of this build), on the HIP cache-write kernel:
+        slot = block * bs + offset, either cache layout.
         """
         if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
             return
-        n = slot_mapping.shape[0]
-        pc = PagedCache.from_tensor(kv_cache)
-        slot = slot_mapping.long()
-        blk = torch.div(slot, pc.block_size, rounding_mode="floor")
-        off = slot % pc.block_size
-        d = pc.head_dim
-        if pc.layout == "v031":
-            kv_cache[blk, :, off, :d] = key[:n]
-            kv_cache[blk, :, off, d:] = value[:n]
-        else:
-            kv_cache[blk, 0, off] = key[:n]
-            kv_cache[blk, 1, off] = value[:n]
+        reshape_and_cache(key, value, kv_cache, slot_mapping)
 
     # -- planning -------------------------------------------------------------
     def _peer_for_request(self, first_block: int, layer_name: str, n_reqs: int):

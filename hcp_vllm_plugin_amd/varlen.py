@@ -98,6 +98,7 @@ def segment_contiguous(k: torch.Tensor, v: torch.Tensor, start: int = 0,
     s.start = start
     s.len = n
     s.block_size = 0
+    s._keep = (k, v)  # the descriptor holds raw addresses: keep the storage alive
     return s
 
 
@@ -140,6 +141,7 @@ def segment_paged(pc: PagedCache, block_table_row: torch.Tensor, start: int,
     s.start = start
     s.len = length
     s.block_size = pc.block_size
+    s._keep = (pc.cache, block_table_row)  # raw addresses inside: keep them alive
     return s
 
 
@@ -149,6 +151,7 @@ def make_entry(q_start: int, q_len: int, seg: KvSegment, causal_offset: int = 0)
     e.q_len = q_len
     e.causal_offset = causal_offset
     e.kv = seg
+    e._keep = getattr(seg, "_keep", None)
     return e
 
 
@@ -199,6 +202,9 @@ class VarlenLaunch:
         self.entries_dev = _to_device(arr, device)
         self.tiles_dev = _to_device(tiles, device)
         self.device = device
+        # the entries point at K/V / cache / block-table storage by address:
+        # hold those tensors for as long as this launch can run
+        self._keep = [getattr(e, "_keep", None) for e in entries]
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
             num_kv_heads: int, scale: float) -> None:
@@ -302,6 +308,8 @@ class DecodeBatch:
         self.starts_dev = _to_device(starts, device)
         self.ws_bytes = int(L.hcp_decode_workspace_bytes(max(rc, 1), num_heads, head_dim))
         self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+        # the segments point at K/V / cache / block-table storage by address
+        self._keep = [getattr(e, "_keep", None) for e in entries]
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
             scale: float) -> None:

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 2
+#define HCP_ABI_VERSION 3
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -47,7 +47,9 @@ typedef enum hcp_status {
 typedef enum hcp_dtype {
   HCP_DTYPE_F16 = 0,
   HCP_DTYPE_BF16 = 1,
-  HCP_DTYPE_F32 = 2 /* only for merge inputs/outputs */
+  HCP_DTYPE_F32 = 2, /* only for merge inputs/outputs */
+  HCP_DTYPE_I32 = 3, /* index arrays (slot_mapping) */
+  HCP_DTYPE_I64 = 4
 } hcp_dtype;
 
 /*
@@ -232,6 +234,46 @@ int hcp_merge_attn_states(void* out, int64_t o_stride_tok,
                           const float* suffix_lse, int64_t s_lse_stride_head,
                           int64_t num_tokens, int32_t num_heads,
                           int32_t head_dim, void* stream);
+
+/*
+ * A paged KV cache: token `off` of block `blk`, KV head `h` lives at
+ * k_addr + (blk * stride_block + h * stride_head + off * stride_tok) elements
+ * (same for V at v_addr).  vLLM 0.31 [nb, Hkv, bs, 2*D]: v_addr = k_addr + D,
+ * stride_block = Hkv*bs*2D, stride_head = bs*2D, stride_tok = 2D
+ * (file_connector.py:13-16); vLLM 0.23 [nb, 2, bs, Hkv, D]: v_addr = k_addr +
+ * bs*Hkv*D, stride_block = 2*bs*Hkv*D, stride_head = D, stride_tok = Hkv*D
+ * (ring_backend.py:601).  block_size is a power of two.
+ */
+typedef struct hcp_paged_cache {
+  uint64_t k_addr;
+  uint64_t v_addr;
+  int64_t stride_block;
+  int64_t stride_head;
+  int64_t stride_tok;
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t reserved;
+} hcp_paged_cache;
+
+/*
+ * Paged KV-cache write: key/value rows t < num_tokens ([num_tokens, Hkv, D],
+ * dtype) go to slot slot_mapping[t] = block * block_size + offset of the
+ * cache.  Replaces the torch index assignment of do_kv_cache_update
+ * (ring_backend.py:501-539; key_cache[block_idx, block_off] = key[:n]).  A
+ * negative slot is a padding token and is skipped (vLLM reshape_and_cache
+ * convention; the reference has no padding slots); a slot >= num_blocks *
+ * block_size is skipped too.  slot_mapping is a DEVICE array of
+ * HCP_DTYPE_I32 or HCP_DTYPE_I64; `cache` is a HOST pointer to the
+ * descriptor.  head_dim must be a multiple of 8; rows and the cache must be
+ * 16-byte aligned with strides that are multiples of 8 elements.
+ */
+int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok,
+                          int64_t k_stride_head, const void* value,
+                          int64_t v_stride_tok, int64_t v_stride_head,
+                          const void* slot_mapping, int32_t slot_dtype,
+                          int64_t num_tokens, int32_t num_kv_heads,
+                          int32_t head_dim, const hcp_paged_cache* cache,
+                          int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

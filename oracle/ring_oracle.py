@@ -19,6 +19,11 @@ order, the reference's plain-PyTorch path of stark-sim/hcp-vllm-plugin:
   for the vLLM 0.23 layout ``[nb, 2, bs, Hkv, D]`` and the vLLM 0.31 layout
   ``[nb, Hkv, bs, 2*D]`` (file_connector.py:13-16,175-179: K is ``[..., :D]``,
   V is ``[..., D:]``).
+* ``kv_cache_update``    <- ``do_kv_cache_update`` ring_backend.py:501-539: slot =
+  block * bs + offset, ``key_cache[block_idx, block_off] = key[:n]`` (and V)
+  for the 0.23 layout, the same rows of the 0.31 layout's ``[..., :D]`` /
+  ``[..., D:]`` halves.  A negative slot (vLLM's padding convention; the
+  reference never passes one) is skipped -- parity unpinned for that case.
 * ``ring_forward``       <- the segmentation of ``HcpRingAttentionImpl.forward``
   ring_backend.py:576-834 (non-decode-ring branch): vanilla causal when there is
   no peer, ``n_a`` queries inside the peer region, local causal at offset
@@ -54,6 +59,7 @@ __all__ = [
     "merge_pair",
     "merge_attn_states",
     "gather_paged",
+    "kv_cache_update",
     "ring_forward",
     "causal_pairs",
     "attn_flops",
@@ -179,6 +185,40 @@ def merge_attn_states(
     output.copy_(out.to(output.dtype))
     if output_lse is not None:
         output_lse.copy_(lse)
+
+
+def kv_cache_update(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    kv_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    layout: str,
+) -> None:
+    """Write key/value rows ``[0, n)`` (n = len(slot_mapping)) into ``kv_cache``
+    in place at slot = block * bs + offset (ring_backend.py:501-539).
+
+    ``layout="v023"``: ``[nb, 2, bs, Hkv, D]``, key_cache / value_cache =
+    ``kv_cache.unbind(1)`` (ring_backend.py:533-538).  ``layout="v031"``:
+    ``[nb, Hkv, bs, 2*D]`` with K in ``[..., :D]``, V in ``[..., D:]``
+    (file_connector.py:13-16).  Negative slots are skipped.
+    """
+    n = slot_mapping.shape[0]
+    keep = slot_mapping >= 0
+    slot = slot_mapping[keep].long()
+    k, v = key[:n][keep], value[:n][keep]
+    bs = kv_cache.shape[2]
+    block_idx = torch.div(slot, bs, rounding_mode="floor")
+    block_off = slot % bs
+    if layout == "v023":
+        key_cache, value_cache = kv_cache.unbind(1)
+        key_cache[block_idx, block_off] = k
+        value_cache[block_idx, block_off] = v
+    elif layout == "v031":
+        d = kv_cache.shape[3] // 2
+        kv_cache[block_idx, :, block_off, :d] = k
+        kv_cache[block_idx, :, block_off, d:] = v
+    else:
+        raise ValueError(layout)
 
 
 def gather_paged(

@@ -63,6 +63,8 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(VarlenEntry) == 96
     assert ctypes.sizeof(DecodeSplit) == 16
     assert VarlenEntry.kv.offset == 24
+    # hcp_paged_cache: 2 u64 + 4 i64 + 2 i32 = 56 bytes
+    assert ctypes.sizeof(_lib.PagedCacheDesc) == 56
 
 
 def _entry(q_start, q_len, off, kv_len, start=0):
@@ -205,6 +207,42 @@ def test_argument_validation_status_codes(L):
     rc = L.hcp_merge_attn_states(16, 8, 8, 1, None, 0, 16, 8, 8, 1, 16, 4, 16, 8, 8, 1, 16, 4,
                                  4, 1, 12, None)
     assert rc == _lib.HCP_EUNSUPPORTED  # head_dim 12
+
+
+def _cache_desc(bs=16, nb=4):
+    c = _lib.PagedCacheDesc()
+    c.k_addr, c.v_addr = 0x1000, 0x1100
+    c.stride_block, c.stride_head, c.stride_tok = 4 * bs * 256, bs * 256, 256
+    c.num_blocks, c.block_size = nb, bs
+    return c
+
+
+def _rc(L, **kw):
+    a = dict(key=16, value=16, kst=512, khst=128, slots=16, sdt=_lib.DTYPE_I64, n=4, hkv=4,
+             d=128, cache=_cache_desc(), dtype=_lib.DTYPE_BF16)
+    a.update(kw)
+    c = a["cache"]
+    return L.hcp_reshape_and_cache(a["key"], a["kst"], a["khst"], a["value"], a["kst"],
+                                   a["khst"], a["slots"], a["sdt"], a["n"], a["hkv"], a["d"],
+                                   ctypes.byref(c) if c is not None else None, a["dtype"], None)
+
+
+def test_reshape_and_cache_status_codes(L):
+    """Argument checks of the cache write, all returned before any launch."""
+    assert _rc(L, n=0) == _lib.HCP_OK                       # nothing to write
+    assert _rc(L, cache=_cache_desc(nb=0)) == _lib.HCP_OK   # empty cache
+    assert _rc(L, d=96) == _lib.HCP_EUNSUPPORTED
+    assert _rc(L, dtype=_lib.DTYPE_F32) == _lib.HCP_EUNSUPPORTED
+    assert _rc(L, sdt=_lib.DTYPE_BF16) == _lib.HCP_EUNSUPPORTED
+    assert b"slot dtype" in L.hcp_last_error()
+    assert _rc(L, cache=None) == _lib.HCP_EINVAL
+    assert _rc(L, cache=_cache_desc(bs=12)) == _lib.HCP_EINVAL
+    assert b"power of two" in L.hcp_last_error()
+    assert _rc(L, key=None) == _lib.HCP_EINVAL
+    assert _rc(L, slots=None) == _lib.HCP_EINVAL
+    assert _rc(L, value=24) == _lib.HCP_EINVAL              # not 16-byte aligned
+    assert _rc(L, kst=500) == _lib.HCP_EINVAL               # stride not a multiple of 8
+    assert _rc(L, n=-1) == _lib.HCP_EINVAL
 
 
 def test_check_raises_runtime_error_with_library_text(L):

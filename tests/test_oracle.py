@@ -226,6 +226,50 @@ def test_gather_paged(layout):
             assert torch.equal(k[t, h], ek) and torch.equal(v[t, h], ev)
 
 
+@pytest.mark.parametrize("layout", ["v023", "v031"])
+def test_kv_cache_update_vs_elementwise_and_gather(layout):
+    """kv_cache_update writes slot = block * bs + offset: checked element by
+    element against explicit loops, padding (-1) slots left untouched, and
+    read back through gather_paged (pinned above) along a block table."""
+    gen = torch.Generator().manual_seed(9)
+    nb, bs, hkv, d, n = 10, 4, 2, 8, 23
+    shape = (nb, 2, bs, hkv, d) if layout == "v023" else (nb, hkv, bs, 2 * d)
+    cache = rnd(gen, *shape)
+    before = cache.clone()
+    key, value = rnd(gen, n + 3, hkv, d), rnd(gen, n + 3, hkv, d)  # padded rows
+    slots = torch.randperm(nb * bs, generator=gen)[:n].clone()
+    slots[[2, 11]] = -1
+    orc.kv_cache_update(key, value, cache, slots, layout)
+    written = set()
+    for t in range(n):
+        s = int(slots[t])
+        if s < 0:
+            continue
+        b, o = s // bs, s % bs
+        written.add((b, o))
+        for h in range(hkv):
+            if layout == "v023":
+                gk, gv = cache[b, 0, o, h], cache[b, 1, o, h]
+            else:
+                gk, gv = cache[b, h, o, :d], cache[b, h, o, d:]
+            assert torch.equal(gk, key[t, h]) and torch.equal(gv, value[t, h])
+    for b in range(nb):
+        for o in range(bs):
+            if (b, o) in written:
+                continue
+            if layout == "v023":
+                assert torch.equal(cache[b, :, o], before[b, :, o])
+            else:
+                assert torch.equal(cache[b, :, o], before[b, :, o])
+    # round trip: tokens written along a block table come back from gather_paged
+    row = torch.randperm(nb, generator=gen).to(torch.int32)
+    length = 13
+    tok_slots = torch.tensor([int(row[x // bs]) * bs + x % bs for x in range(length)])
+    orc.kv_cache_update(key, value, cache, tok_slots, layout)
+    k, v = orc.gather_paged(cache, row, 0, length, layout)
+    assert torch.equal(k, key[:length]) and torch.equal(v, value[:length])
+
+
 def _full_causal(q, k, v, scale, qpos0):
     return brute(q, k, v, scale, qpos0)[0]
 
