@@ -288,6 +288,60 @@ def bench_kv_cache_write(dev, steps, warmup, seed=2, n=43125, nb=12000, bs=16):
     }
 
 
+def bench_peer_ingest(dev, steps, warmup, chunks=(4096, 4096), fmt="k_v"):
+    """Peer-KV ingest of one layer: a request's chunk files (ring connector
+    {"k","v"}: [n, 4, 128] bf16 safetensors, in the page cache) into one packed
+    device buffer, against the reference's way -- safetensors load_file to
+    the device per chunk, .contiguous(), torch.cat (ring_connector.py:908-915,
+    ring_backend.py:766-772).  Wall clock per layer, copies complete."""
+    import tempfile
+
+    import safetensors.torch as st
+    from hcp_vllm_plugin_amd.peer_ingest import PeerIngest
+
+    gen = torch.Generator().manual_seed(5)
+    tmp = tempfile.mkdtemp(prefix="hcp_ingest_")
+    paths = []
+    for i, n in enumerate(chunks):
+        p = os.path.join(tmp, f"layer0_chunk{i}.safetensors")
+        st.save_file({"k": torch.randn(n, HKV, D, generator=gen).to(torch.bfloat16),
+                      "v": torch.randn(n, HKV, D, generator=gen).to(torch.bfloat16)}, p)
+        paths.append(p)
+    ing = PeerIngest(dev, fmt)
+
+    def ours():
+        r = ing.load(paths)
+        r.event.synchronize()
+
+    def ref():
+        parts = [st.load_file(p, device=str(dev)) for p in paths]
+        k = torch.cat([t["k"].contiguous() for t in parts])
+        v = torch.cat([t["v"].contiguous() for t in parts])
+        torch.cuda.synchronize()
+        return k, v
+
+    def wall(fn):
+        for _ in range(warmup):
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    ms, ms_ref = wall(ours), wall(ref)
+    byts = sum(chunks) * HKV * D * 2 * 2
+    for p in paths:
+        os.remove(p)
+    os.rmdir(tmp)
+    return {
+        "workload": (f"peer-KV ingest of one layer: {len(chunks)} chunk files of "
+                     f"{list(chunks)} tokens ([n,4,128] bf16 k and v) into one packed device "
+                     f"buffer, vs safetensors load_file(device) + torch.cat"),
+        "ms": round(ms, 4), "gbs": round(byts / (ms * 1e-3) / 1e9, 2),
+        "reference_way_ms": round(ms_ref, 4), "bytes": byts,
+    }
+
+
 def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
     """Long-context layer at the Llama-3-70B attention shape (64 / 8 heads,
     head_dim 128), bf16: 65536 local query tokens causal over local keys
@@ -433,7 +487,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
-                                       "kvwrite", "copy"),
+                                       "kvwrite", "ingest", "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -457,6 +511,9 @@ def main():
     if args.part == "varlen":
         print(json.dumps(bench_varlen(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "ingest":
+        print(json.dumps(bench_peer_ingest(dev, args.steps, args.warmup)), flush=True)
+        return
     if args.part == "kvwrite":
         print(json.dumps(bench_kv_cache_write(dev, args.steps, args.warmup)), flush=True)
         return
@@ -473,6 +530,7 @@ def main():
         extra["varlen16_paged"] = bench_varlen(dev, args.steps, args.warmup)
         extra["llama70b_128k"] = bench_llama70b(dev, 2, 1)
         extra["kv_cache_write"] = bench_kv_cache_write(dev, args.steps, args.warmup)
+        extra["peer_ingest"] = bench_peer_ingest(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 
