@@ -342,6 +342,65 @@ def bench_peer_ingest(dev, steps, warmup, chunks=(4096, 4096), fmt="k_v"):
     }
 
 
+def bench_ring_decode_hop(dev, steps, warmup, seed=6, chunk=32768, growth=512):
+    """One decode-ring hop at Qwen2.5-7B shape (q [1,28,128] bf16): a node's
+    partial over its 32768-key chunk snapshot + 512 growth tokens merged into
+    the accumulator with LSE out.  ``ms`` is the device step (split-KV decode
+    over [chunk, growth] + merge); ``packet_ms`` the whole ``handle_packet``
+    (decode the packet, uploads, the step, one download, re-encode), wall
+    clock.  ``reference_way_ms`` runs the reference's structure
+    (ring_decode.py:224-237: torch.cat of chunk and growth, the prefill kernel
+    with Tq=1, merge_attn_states, the LSE in four torch ops) on this build's
+    kernels, for comparison."""
+    from hcp_vllm_plugin_amd import ring_decode as rd
+    from hcp_vllm_plugin_amd.merge import merge_attn_states
+    from hcp_vllm_plugin_amd.ring_attn import ring_attn_with_lse
+
+    dgen = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*shape):
+        return torch.randn(*shape, generator=dgen, device=dev).to(torch.bfloat16)
+
+    ck, cv = rn(chunk, HKV, D), rn(chunk, HKV, D)
+    node = rd.RingDecodeNode("", ["c"], 1, device=str(dev), dtype=torch.bfloat16,
+                             background=False)
+    node.add_chunk("c", "L", ck, cv)
+    node.mark_ready()
+    gk, gv = rn(growth, HKV, D), rn(growth, HKV, D)
+    node.append_growth("r", "L", gk, gv)
+    q, o0 = rn(1, H, D), rn(1, H, D)
+    l0 = torch.randn(H, 1, generator=dgen, device=dev)
+    sc = 1.0 / math.sqrt(D)
+    ms = timed(lambda: node.accumulate(q, o0, l0, sc, "L", "r"), steps, warmup)
+
+    def ref_way():
+        k = torch.cat([ck, gk], 0)
+        v = torch.cat([cv, gv], 0)
+        o_loc, lse_loc = ring_attn_with_lse(q, k, v, sc, None)
+        out = torch.empty_like(o0)
+        merge_attn_states(out, o0, l0, o_loc, lse_loc)
+        m = torch.maximum(l0, lse_loc)
+        return out, m + torch.log(torch.exp(l0 - m) + torch.exp(lse_loc - m))
+
+    ms_ref = timed(ref_way, steps, warmup)
+    pkt = rd.encode_packet(q, o0, l0, sc, "L", "c", "r")
+    for _ in range(warmup):
+        node.handle_packet(pkt)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        node.handle_packet(pkt)
+    packet_ms = (time.perf_counter() - t0) * 1e3 / steps
+    byts = (chunk + growth) * HKV * D * 2 * 2
+    return {
+        "workload": (f"decode-ring hop: q [1,28,128] bf16 over a {chunk}-key chunk snapshot + "
+                     f"{growth} growth tokens ([n,4,128] k and v), merged with LSE out"),
+        "ms": round(ms, 4), "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "bytes": byts, "packet_ms": round(packet_ms, 4),
+        "reference_way_ms": round(ms_ref, 4),
+    }
+
+
 def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
     """Long-context layer at the Llama-3-70B attention shape (64 / 8 heads,
     head_dim 128), bf16: 65536 local query tokens causal over local keys
@@ -487,7 +546,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
-                                       "kvwrite", "ingest", "copy"),
+                                       "kvwrite", "ingest", "ringdec", "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -514,6 +573,9 @@ def main():
     if args.part == "ingest":
         print(json.dumps(bench_peer_ingest(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "ringdec":
+        print(json.dumps(bench_ring_decode_hop(dev, args.steps, args.warmup)), flush=True)
+        return
     if args.part == "kvwrite":
         print(json.dumps(bench_kv_cache_write(dev, args.steps, args.warmup)), flush=True)
         return
@@ -531,6 +593,7 @@ def main():
         extra["llama70b_128k"] = bench_llama70b(dev, 2, 1)
         extra["kv_cache_write"] = bench_kv_cache_write(dev, args.steps, args.warmup)
         extra["peer_ingest"] = bench_peer_ingest(dev, args.steps, args.warmup)
+        extra["ring_decode_hop"] = bench_ring_decode_hop(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 

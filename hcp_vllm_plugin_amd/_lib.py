@@ -51,11 +51,12 @@ EXPORTED_SYMBOLS = (
     "hcp_plan_decode_splits",
     "hcp_decode_workspace_bytes",
     "hcp_decode_splitkv",
+    "hcp_decode_splitkv_acc",
     "hcp_merge_attn_states",
     "hcp_reshape_and_cache",
 )
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class KvSegment(ctypes.Structure):
@@ -148,6 +149,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_decode_splitkv.restype = ctypes.c_int
     lib.hcp_decode_splitkv.argtypes = [
         _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I32, _P, ctypes.c_size_t,
+        _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _F, _I32, _P,
+    ]
+    lib.hcp_decode_splitkv_acc.restype = ctypes.c_int
+    lib.hcp_decode_splitkv_acc.argtypes = [
+        _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I32, _P, ctypes.c_size_t,
+        _P, _I64, _I64, _P, _I64,
         _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _F, _I32, _P,
     ]
     lib.hcp_reshape_and_cache.restype = ctypes.c_int

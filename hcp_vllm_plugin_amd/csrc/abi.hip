@@ -254,15 +254,16 @@ size_t hcp_decode_workspace_bytes(int32_t num_splits, int32_t num_heads, int32_t
   return o_al + n * sizeof(float);
 }
 
-int hcp_decode_splitkv(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
-                       const hcp_varlen_entry* entries, int32_t num_entries,
-                       const hcp_decode_split* splits, int32_t num_splits,
+static int decode_impl(const char* who, const void* q, int64_t q_stride_tok,
+                       int64_t q_stride_head, const hcp_varlen_entry* entries,
+                       int32_t num_entries, const hcp_decode_split* splits, int32_t num_splits,
                        const int32_t* seq_partial_start, int32_t num_seqs, void* workspace,
                        size_t workspace_bytes, void* out, int64_t o_stride_tok,
                        int64_t o_stride_head, float* lse, int64_t lse_stride_head,
-                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
-                       int32_t dtype, void* stream) {
-  const char* who = "hcp_decode_splitkv";
+                       const void* acc_o, int64_t acc_stride_tok, int64_t acc_stride_head,
+                       const float* acc_lse, int64_t acc_lse_stride_head, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, float scale, int32_t dtype,
+                       void* stream) {
   int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
   if (rc) return rc;
   if (num_heads / num_kv_heads > 16)
@@ -308,8 +309,49 @@ int hcp_decode_splitkv(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
   rp.lse = lse;
   rp.lse_stride_head = lse_stride_head;
   rp.num_heads = num_heads;
+  rp.acc_o = acc_o;
+  rp.acc_stride_tok = acc_stride_tok;
+  rp.acc_stride_head = acc_stride_head;
+  rp.acc_lse = acc_lse;
+  rp.acc_lse_stride_head = acc_lse_stride_head;
   hipError_t e = hcp::launch_decode(dp, rp, head_dim, dtype, static_cast<hipStream_t>(stream));
   return launch_status(e, who);
+}
+
+int hcp_decode_splitkv(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                       const hcp_varlen_entry* entries, int32_t num_entries,
+                       const hcp_decode_split* splits, int32_t num_splits,
+                       const int32_t* seq_partial_start, int32_t num_seqs, void* workspace,
+                       size_t workspace_bytes, void* out, int64_t o_stride_tok,
+                       int64_t o_stride_head, float* lse, int64_t lse_stride_head,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                       int32_t dtype, void* stream) {
+  return decode_impl("hcp_decode_splitkv", q, q_stride_tok, q_stride_head, entries,
+                     num_entries, splits, num_splits, seq_partial_start, num_seqs, workspace,
+                     workspace_bytes, out, o_stride_tok, o_stride_head, lse, lse_stride_head,
+                     nullptr, 0, 0, nullptr, 0, num_heads, num_kv_heads, head_dim, scale,
+                     dtype, stream);
+}
+
+int hcp_decode_splitkv_acc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                           const hcp_varlen_entry* entries, int32_t num_entries,
+                           const hcp_decode_split* splits, int32_t num_splits,
+                           const int32_t* seq_partial_start, int32_t num_seqs,
+                           void* workspace, size_t workspace_bytes, const void* acc_o,
+                           int64_t acc_stride_tok, int64_t acc_stride_head,
+                           const float* acc_lse, int64_t acc_lse_stride_head, void* out,
+                           int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+                           int64_t lse_stride_head, int32_t num_heads, int32_t num_kv_heads,
+                           int32_t head_dim, float scale, int32_t dtype, void* stream) {
+  const char* who = "hcp_decode_splitkv_acc";
+  if (!acc_o || !acc_lse) return fail(HCP_EINVAL, "%s: null accumulator", who);
+  if (reinterpret_cast<uintptr_t>(acc_o) % 2)
+    return fail(HCP_EINVAL, "%s: acc_o not 2-byte aligned", who);
+  return decode_impl(who, q, q_stride_tok, q_stride_head, entries, num_entries, splits,
+                     num_splits, seq_partial_start, num_seqs, workspace, workspace_bytes, out,
+                     o_stride_tok, o_stride_head, lse, lse_stride_head, acc_o, acc_stride_tok,
+                     acc_stride_head, acc_lse, acc_lse_stride_head, num_heads, num_kv_heads,
+                     head_dim, scale, dtype, stream);
 }
 
 int hcp_merge_attn_states(void* out, int64_t o_stride_tok, int64_t o_stride_head,

@@ -320,23 +320,74 @@ decode_split_kernel(DecParams p) {
     decode_split_body<D, T, false>(p, kvh, sp, e, spl, bufE, bufO, sm_m, sm_l);
 }
 
+// Merge every partial of one (sequence, query head) -- and the running
+// accumulator, when given -- into the output row and its LSE.  One workgroup
+// of D threads per (sequence, head), thread d owns column d.  The max over
+// partial LSEs is thread-strided plus a block reduction; the weighted sum
+// issues 8 partials' loads before consuming them, so a long sequence (one
+// request split over the whole machine) is not a chain of dependent loads.
 template <int D, typename T>
 __global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
+  constexpr int kWaves = D / 64;
+  __shared__ float sm_max[kWaves];
   const int sh = blockIdx.x;
   const int seq = sh / p.num_heads, head = sh % p.num_heads;
   const int d = threadIdx.x;
   const int p0 = p.seq_partial_start[seq], p1 = p.seq_partial_start[seq + 1];
-  float M = -INFINITY;
-  for (int i = p0; i < p1; ++i)
-    M = fmaxf(M, p.ws_lse[static_cast<int64_t>(i) * p.num_heads + head]);
+  const int n = p1 - p0;
+  const int64_t lstep = p.num_heads;
+  const float* lcol = p.ws_lse + static_cast<int64_t>(p0) * lstep + head;
+  const int64_t ostep = lstep * D;
+  const float* ocol = p.ws_o + (static_cast<int64_t>(p0) * lstep + head) * D + d;
+
+  // accumulator first: out / lse may alias acc_o / acc_lse, and every read
+  // of them happens before the barrier below, every write after it
+  float acc_l = -INFINITY, acc_v = 0.f;
+  if (p.acc_lse != nullptr) {
+    acc_l = p.acc_lse[static_cast<int64_t>(head) * p.acc_lse_stride_head + seq];
+    if (acc_l == INFINITY) acc_l = -INFINITY;  // merge_attn_states reads +inf as empty
+    const uint16_t* arow = reinterpret_cast<const uint16_t*>(p.acc_o) +
+                           seq * p.acc_stride_tok + static_cast<int64_t>(head) * p.acc_stride_head;
+    acc_v = Elem<T>::to_float(arow[d]);
+  }
+
+  float m = -INFINITY;
+  for (int i = d; i < n; i += D) m = fmaxf(m, lcol[i * lstep]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((d & 63) == 0) sm_max[d >> 6] = m;
+  __syncthreads();
+  float M = acc_l;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_max[w]);
+
   float o = 0.f, lse = -INFINITY;
   if (M != -INFINITY) {
     float S = 0.f, O = 0.f;
-    for (int i = p0; i < p1; ++i) {
-      const int64_t slot = static_cast<int64_t>(i) * p.num_heads + head;
-      const float w = __expf(p.ws_lse[slot] - M);
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+      float l[8], v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        l[j] = lcol[(i + j) * lstep];
+        v[j] = ocol[(i + j) * ostep];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float w = __expf(l[j] - M);
+        S += w;
+        O += w * v[j];
+      }
+    }
+    for (; i < n; ++i) {
+      const float w = __expf(lcol[i * lstep] - M);
       S += w;
-      O += w * p.ws_o[slot * D + d];
+      O += w * ocol[i * ostep];
+    }
+    if (acc_l != -INFINITY) {
+      const float w = __expf(acc_l - M);
+      S += w;
+      O += w * acc_v;
     }
     o = O / S;
     lse = M + __logf(S);

@@ -47,6 +47,11 @@ struct RedParams {
   float* lse;
   int64_t lse_stride_head;
   int32_t num_heads;
+  // optional running accumulator merged in as one more partial (NULL: none)
+  const void* acc_o;
+  int64_t acc_stride_tok, acc_stride_head;
+  const float* acc_lse;
+  int64_t acc_lse_stride_head;
 };
 
 struct MergeParams {

@@ -26,6 +26,14 @@ Drop-in for hcp_vllm_plugin/ring_backend.py's hot path:
 * The peer-KV staging input contract (ring_backend.py:78-136):
   ``PEER_KV_STAGING[(chunk_key, layer_name)] = (k, v)`` with k/v
   ``[n, Hkv, D]`` post-RoPE, ``PEER_REQ_MAP[first_block_id] = [chunk keys]``.
+* Memory-split decode (accumulator ring, ring_backend.py:140-227, :632-722):
+  ``register_decode_ring`` / ``clear_decode_ring`` / ``DECODE_RING_MAP``.  A
+  registered request's single-token decode step skips the pool write, and its
+  attention is the owner's local partial (own chunk in the pool + owned growth
+  + current token) sent around the ring by ``ring_decode.ring_decode_step``;
+  decode growth is sharded by ``ring_decode.growth_assignee``.  In a pure
+  decode batch the owner partials run in the same split-KV launch as the
+  other rows.
 * ``IMPL_STATS`` evidence counters (ring_backend.py:295-306).  ``attn_hip`` /
   ``merge_hip`` count kernel launches; the legacy keys ``attn_triton`` /
   ``merge_triton`` mirror them so validators that read those names still see
@@ -44,6 +52,7 @@ from . import _lib
 from .kv_cache import reshape_and_cache
 from .merge import merge_attn_states
 from .ring_attn import ring_attn_with_lse
+from .ring_decode import GrowthBuffer, growth_assignee, local_partial, ring_decode_step
 from .varlen import (
     DecodeBatch,
     PagedCache,
@@ -117,6 +126,95 @@ def clear_peer_kv() -> None:
 
 
 # ---------------------------------------------------------------------------
+# Memory-split decode registry (ring_backend.py:140-227)
+# ---------------------------------------------------------------------------
+DECODE_RING_MAP: dict[int, dict] = {}
+_STAGING_RELEASE_FN = None
+
+
+def _decode_ring_enabled() -> bool:
+    return os.environ.get("HCP_RING_DECODE_RING", "1") == "1"
+
+
+def _growth_policy() -> str:
+    return os.environ.get("HCP_RING_DECODE_GROWTH", "rr")
+
+
+def set_staging_release_fn(fn) -> None:
+    """Connector callback that frees a request's staged prefix KV."""
+    global _STAGING_RELEASE_FN
+    _STAGING_RELEASE_FN = fn
+
+
+def register_decode_ring(first_block_id: int, peer_chunks: list[tuple[str, str]],
+                         prefix_len: int, transport=None) -> None:
+    """Switch a request to memory-split decode (ring_backend.py:175-208).
+
+    ``peer_chunks``: ordered ``(chunk_key, peer_url)`` of the prefix (entries
+    with an empty url are dropped); ``prefix_len``: tokens of the prefix;
+    ``transport``: the ring transport (``send_packet`` / ``recv_packet``).
+    Ring indices: 0..N-2 the prefix peers, N-1 the owner.
+    """
+    import uuid
+
+    peers = [(ck, u) for ck, u in peer_chunks if u]
+    DECODE_RING_MAP[first_block_id] = {
+        "peer_chunks": peers,
+        "prefix_len": prefix_len,
+        "req_tag": f"{first_block_id}:{uuid.uuid4().hex[:8]}",
+        "ring_size": len(peers) + 1,
+        "own_index": len(peers),
+        "own_chunk_len": None,     # set at the first decode step
+        "growth": {},              # layer -> GrowthBuffer (owner's share)
+        "pending_growth": {},      # layer -> (assignee, k, v), shipped next step
+        "growth_policy": _growth_policy(),
+        "transport": transport,
+    }
+
+
+def clear_decode_ring(first_block_id: int) -> None:
+    DECODE_RING_MAP.pop(first_block_id, None)
+
+
+def _release_staged_for_request(first_block_id: int) -> None:
+    """Free a request's staged prefix KV at its decode-ring transition
+    (ring_backend.py:214-225)."""
+    if first_block_id not in PEER_REQ_MAP:
+        return
+    if _STAGING_RELEASE_FN is not None:
+        _STAGING_RELEASE_FN(first_block_id)
+    else:
+        for ck in PEER_REQ_MAP.pop(first_block_id, None) or []:
+            drop_chunk_kv(ck)
+
+
+def _forward_attn_metadata(layer):
+    """This step's attention metadata for ``layer`` from vLLM's forward
+    context, or None (no vLLM, or no context)."""
+    try:
+        from vllm.forward_context import get_forward_context  # type: ignore
+
+        raw = get_forward_context().attn_metadata
+    except Exception:  # noqa: BLE001 -- no context: attribute nothing
+        return None
+    if isinstance(raw, dict):
+        return raw.get(layer.layer_name)
+    if isinstance(raw, list):
+        return raw[0].get(layer.layer_name)
+    return raw
+
+
+# Pool-write evidence (ring_backend.py:260-267): decode-ring tokens skipped.
+WRITE_TRACK: dict = {"enabled": False, "slots": set(), "skipped": 0}
+
+
+def enable_write_tracking() -> None:
+    WRITE_TRACK["enabled"] = True
+    WRITE_TRACK["slots"] = set()
+    WRITE_TRACK["skipped"] = 0
+
+
+# ---------------------------------------------------------------------------
 # Switches and evidence counters
 # ---------------------------------------------------------------------------
 BATCH_STATS: dict = {"max_reqs": 0}
@@ -125,6 +223,7 @@ IMPL_STATS: dict = {
     "attn_hip": 0,
     "merge_hip": 0,
     "decode_hip": 0,
+    "ring_decode_steps": 0,
     "attn_triton": 0,
     "merge_triton": 0,
     "attn_torch": 0,
@@ -242,6 +341,7 @@ class _Plan:
         self.local: list = []           # causal entries over the paged cache
         self.peer_rounds: list = []     # per round: {"contig": [...], "paged": [...]}
         self.any_peer = False
+        self.ring: list = []  # decode-ring rows: (r, q row, tk, ring state, bt row, block 0)
 
 
 class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
@@ -296,13 +396,38 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
     ) -> None:
         """Write this step's K/V into the paged cache at ``slot_mapping``.
 
-        ring_backend.py:501-539 (without the decode-ring skip, whose ring
-        transport is not part of this build), on the HIP cache-write kernel:
-        slot = block * bs + offset, either cache layout.
+        ring_backend.py:501-539 on the HIP cache-write kernel: slot = block *
+        bs + offset, either cache layout.  The single-token decode steps of
+        decode-ring requests are not written (their KV is decode growth,
+        routed by the ring): those rows get slot -1, which the kernel skips,
+        instead of three gather copies.
         """
         if self.attn_type in (AttentionType.ENCODER_ONLY, AttentionType.ENCODER):
             return
+        skip = self._decode_ring_skip_positions(layer, slot_mapping)
+        if skip:
+            WRITE_TRACK["skipped"] += len(skip)
+            slot_mapping = slot_mapping.clone()
+            idx = torch.tensor(sorted(skip), dtype=torch.long, device=slot_mapping.device)
+            slot_mapping.index_fill_(0, idx, -1)
         reshape_and_cache(key, value, kv_cache, slot_mapping)
+        if WRITE_TRACK["enabled"]:
+            WRITE_TRACK["slots"].update(s for s in slot_mapping.tolist() if s >= 0)
+
+    def _decode_ring_skip_positions(self, layer, slot_mapping: torch.Tensor) -> set[int]:
+        """Rows of this step's slot_mapping that are decode-ring requests'
+        single-token decode steps (ring_backend.py:541-574); empty when the
+        step's metadata is unavailable (never skip what cannot be attributed)."""
+        if not (_decode_ring_enabled() and DECODE_RING_MAP):
+            return set()
+        meta = _forward_attn_metadata(layer)
+        if meta is None:
+            return set()
+        qsl = meta.query_start_loc.tolist()
+        first = meta.block_table[:, 0].tolist() if meta.block_table.shape[1] else []
+        return {qsl[r] for r in range(len(qsl) - 1)
+                if qsl[r + 1] - qsl[r] == 1 and int(first[r]) in DECODE_RING_MAP
+                and qsl[r] < slot_mapping.shape[0]}
 
     # -- planning -------------------------------------------------------------
     def _peer_for_request(self, first_block: int, layer_name: str, n_reqs: int):
@@ -327,12 +452,18 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
 
     def _plan(self, layer_name, qsl, seq_lens, block_table, first_blocks, pc, split):
         plan = _Plan()
+        ring_on = _decode_ring_enabled() and bool(DECODE_RING_MAP)
         for r in range(len(seq_lens)):
             qs, qe = qsl[r], qsl[r + 1]
             tq, tk = qe - qs, seq_lens[r]
             if tq == 0:
                 continue
             row = block_table[r]
+            if ring_on and tq == 1:
+                dr = DECODE_RING_MAP.get(first_blocks[r])
+                if dr is not None:
+                    plan.ring.append((r, qs, tk, dr, row, first_blocks[r]))
+                    continue
             qpos0 = tk - tq
             staged = None
             if _ring_enabled():
@@ -411,11 +542,77 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         plan = self._plan(layer_name, qsl, seq_lens, block_table, first_blocks, pc, split)
         n = len(seq_lens)
         is_decode = n > 0 and qsl == list(range(n + 1))
+        ring_local = self._ring_local_segments(plan, pc, key, value, layer_name)
         if is_decode:
-            self._forward_decode(query, out, plan, n)
+            lse = self._forward_decode(query, out, plan, n, ring_local)
+            parts = {r: (out[qs:qs + 1], lse[:, qs:qs + 1]) for (r, qs, *_r) in plan.ring}
         else:
-            self._forward_prefill(query, out, plan)
+            if plan.local or plan.any_peer:
+                self._forward_prefill(query, out, plan)
+            parts = {}
+            for (r, qs, *_r) in plan.ring:
+                parts[r] = self._local_partial(query[qs:qs + 1], ring_local[r])
+        for (r, qs, tk, dr, *_r) in plan.ring:
+            o_acc, lse_acc = parts[r]
+            out[qs:qs + 1] = self._ring_step(dr, layer_name, query[qs:qs + 1],
+                                             o_acc, lse_acc)
         return output
+
+    # -- memory-split decode (owner side) ----------------------------------------
+    def _ring_local_segments(self, plan: _Plan, pc: PagedCache, key, value, layer_name):
+        """Owner-side local segments of each decode-ring row: own chunk in the
+        pool, the owner's growth share, the current token (ring_backend.py:
+        643-671), with the growth bookkeeping of :652-689 done here (the
+        current token joins the owner's growth or waits to be shipped)."""
+        segs = {}
+        for (r, qs, tk, dr, row, fb) in plan.ring:
+            _release_staged_for_request(fb)
+            plen = dr["prefix_len"]
+            if dr["own_chunk_len"] is None:
+                dr["own_chunk_len"] = tk - 1 - plen
+            own_len = dr["own_chunk_len"]
+            pos = tk - 1
+            assignee = growth_assignee(pos, dr["ring_size"], dr["growth_policy"])
+            dr["ship"] = dr["pending_growth"].pop(layer_name, None)
+            k_cur = key[qs:qs + 1].contiguous()
+            v_cur = value[qs:qs + 1].contiguous()
+            g = dr["growth"].get(layer_name)
+            if g is None:
+                g = dr["growth"][layer_name] = GrowthBuffer(
+                    self.num_kv_heads, self.head_size, k_cur.dtype, k_cur.device)
+            own = segment_paged(pc, row, plen, own_len) if own_len > 0 else None
+            if assignee == dr["own_index"]:
+                g.append(k_cur, v_cur)
+                segs[r] = [own, g.segment()]
+            else:
+                segs[r] = [own, g.segment(), segment_contiguous(k_cur, v_cur)]
+                dr["pending_growth"][layer_name] = (assignee, k_cur, v_cur)
+        return segs
+
+    def _local_partial(self, q_r, segs):
+        o, lse = local_partial(q_r, segs, self.num_kv_heads, self.scale)
+        _count("decode")
+        return o, lse
+
+    def _ring_step(self, dr, layer_name, q_r, o_acc, lse_acc):
+        """Send the owner's accumulator around the ring (ring_backend.py:
+        690-722); the returned (O, LSE) is the exact attention of the step."""
+        transport = dr.get("transport")
+        if transport is None:
+            raise RuntimeError("HCP decode ring requires a ring transport "
+                               "(register_decode_ring(..., transport=...))")
+        ship = dr.pop("ship", None)
+        gk = gv = None
+        target = -1
+        if ship is not None:
+            gk, gv = ship[1], ship[2]
+            target = ship[0] + 1   # growth index 0..N-2 -> transport index 1..N-1
+        first_chunk = dr["peer_chunks"][0][0] if dr["peer_chunks"] else ""
+        o, _lse = ring_decode_step(transport, q_r, o_acc, lse_acc, self.scale, layer_name,
+                                   first_chunk, req=dr["req_tag"], growth_k=gk,
+                                   growth_v=gv, growth_target=target)
+        IMPL_STATS["ring_decode_steps"] += 1
+        return o
 
     def _forward_prefill(self, query, out, plan: _Plan) -> None:
         dev = query.device
@@ -452,7 +649,9 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc)
         _count("merge")
 
-    def _forward_decode(self, query, out, plan: _Plan, n: int) -> None:
+    def _forward_decode(self, query, out, plan: _Plan, n: int, ring_local=None):
+        """One split-KV launch for the whole decode batch; decode-ring rows
+        get their owner-local partial (with LSE) from the same launch."""
         segs: list[list] = [[] for _ in range(n)]
         for e in plan.local:
             segs[e.q_start].append(e.kv)
@@ -460,6 +659,12 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
             for kind in ("contig", "paged"):
                 for e in rnd[kind]:
                     segs[e.q_start].append(e.kv)
+        lse = None
+        for (r, qs, *_r) in plan.ring:
+            segs[qs] = [s for s in ring_local[r] if s is not None and s.len > 0]
+        if plan.ring:
+            lse = torch.empty((self.num_heads, n), dtype=torch.float32, device=query.device)
         DecodeBatch(segs, self.num_heads, self.num_kv_heads, self.head_size,
-                    query.device).run(query, out, None, self.scale)
+                    query.device).run(query, out, lse, self.scale)
         _count("decode")
+        return lse

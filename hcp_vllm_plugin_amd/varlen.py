@@ -155,10 +155,24 @@ def make_entry(q_start: int, q_len: int, seg: KvSegment, causal_offset: int = 0)
     return e
 
 
-def _to_device(arr, device: torch.device) -> torch.Tensor:
-    """Copy a ctypes array to a device byte tensor."""
-    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
-    return host.to(device)
+def _upload(arrays, device: torch.device):
+    """Copy ctypes arrays to the device in one asynchronous copy from pinned
+    memory on the current stream.
+
+    Returns (device byte tensor, [address of each array on the device]), each
+    array 256-byte aligned.  The pinned block comes from torch's caching host
+    allocator, which keeps it until the copy has completed.
+    """
+    offs, total = [], 0
+    for a in arrays:
+        offs.append(total)
+        total += (ctypes.sizeof(a) + 255) & ~255
+    host = torch.empty(max(total, 256), dtype=torch.uint8, pin_memory=True)
+    base = host.data_ptr()
+    for a, o in zip(arrays, offs):
+        ctypes.memmove(base + o, ctypes.addressof(a), ctypes.sizeof(a))
+    dev = host.to(device, non_blocking=True)
+    return dev, [dev.data_ptr() + o for o in offs]
 
 
 def plan_varlen_tiles(entries: list[VarlenEntry], causal: bool) -> list[tuple[int, int]]:
@@ -179,7 +193,9 @@ class VarlenLaunch:
     """A planned varlen launch: entries and tile list uploaded to the device.
 
     Build once per batch layout; ``run`` may be called repeatedly (e.g. per
-    layer, or per benchmark step) with any q/out/lse of matching rows.
+    layer, or per benchmark step) with any q/out/lse of matching rows.  The
+    plan is uploaded asynchronously on the current stream: run it on that
+    stream (or synchronise first).
     """
 
     def __init__(self, entries: list[VarlenEntry], causal: bool, paged: bool,
@@ -199,8 +215,7 @@ class VarlenLaunch:
                                      int(self.causal), bm, ctypes.addressof(tiles), cap)
         _lib.check(rc, "hcp_plan_varlen_tiles")
         self.num_tiles = rc
-        self.entries_dev = _to_device(arr, device)
-        self.tiles_dev = _to_device(tiles, device)
+        self._plan_dev, (self.entries_ptr, self.tiles_ptr) = _upload([arr, tiles], device)
         self.device = device
         # the entries point at K/V / cache / block-table storage by address:
         # hold those tensors for as long as this launch can run
@@ -217,8 +232,8 @@ class VarlenLaunch:
                 q.data_ptr(), q.stride(0), q.stride(1),
                 out.data_ptr(), out.stride(0), out.stride(1),
                 lse.data_ptr(), lse.stride(0),
-                self.entries_dev.data_ptr(), self.num_entries,
-                self.tiles_dev.data_ptr(), self.num_tiles,
+                self.entries_ptr, self.num_entries,
+                self.tiles_ptr, self.num_tiles,
                 num_heads, num_kv_heads, head_dim, float(scale),
                 int(self.causal), int(self.paged), _lib.dtype_code(q.dtype),
                 _lib.stream_ptr(q.device),
@@ -249,31 +264,37 @@ def varlen_attn_with_lse(
     return out, lse
 
 
-def choose_split_tokens(seg_lens: list[int], num_kv_heads: int,
-                        target_workgroups: int = 1024, minimum: int = 256,
+def choose_split_tokens(seg_lens: list[int], num_kv_heads: int, num_cus: int = 256,
+                        max_rounds: int = 4, round_keys: int = 2048, minimum: int = 64,
                         maximum: int = 16384) -> int:
     """Split size from the batch's total key count.
 
-    Aims at ``target_workgroups`` (split, KV head) workgroups -- 4 per CU on
-    256 CUs, one resident at a time (the split kernel's chunk buffers take
-    128 KB of LDS) -- so the launch drains evenly while each split stays
-    long enough that its fp32 partial is small next to the K/V it
-    summarises.  Rounded to 64 keys.
+    The split kernel runs one workgroup per CU at a time (its chunk buffers
+    take 128 KB of LDS), so the launch is planned in whole rounds of
+    ``num_cus`` (split, KV head) workgroups: one round while the work is
+    small (a single long request -- a decode-ring hop -- spread over the whole
+    machine), up to ``max_rounds`` once each workgroup would stream more than
+    ``round_keys`` keys, so the launch drains evenly while each split stays
+    long enough that its fp32 partial is small next to the K/V it summarises.
+    Rounded up to 64 keys.
     """
     total = sum(seg_lens) * num_kv_heads
     if total == 0:
         return minimum
-    s = -(-total // target_workgroups)
+    rounds = min(max_rounds, max(1, -(-total // (num_cus * round_keys))))
+    s = -(-total // (rounds * num_cus))
     s = ((s + 63) // 64) * 64
     return max(minimum, min(maximum, s))
 
 
 class DecodeBatch:
-    """A planned split-KV decode: entries, splits and workspace on the device.
+    """A planned split-KV decode: entries and splits on the device (the fp32
+    partials' workspace is taken per run).
 
     ``segments[s]`` lists the KV segments of sequence ``s`` (all keys visible
     to its single query, e.g. the staged peer prefix and the local paged KV
-    including the current token).
+    including the current token).  The plan is uploaded asynchronously on the
+    current stream: run it on that stream (or synchronise first).
     """
 
     def __init__(self, segments: list[list[KvSegment]], num_heads: int, num_kv_heads: int,
@@ -303,31 +324,50 @@ class DecodeBatch:
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
-        self.entries_dev = _to_device(arr, device)
-        self.splits_dev = _to_device(splits, device)
-        self.starts_dev = _to_device(starts, device)
+        self._plan_dev, (self.entries_ptr, self.splits_ptr, self.starts_ptr) = _upload(
+            [arr, splits, starts], device)
         self.ws_bytes = int(L.hcp_decode_workspace_bytes(max(rc, 1), num_heads, head_dim))
-        self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+        self.device = device
         # the segments point at K/V / cache / block-table storage by address
         self._keep = [getattr(e, "_keep", None) for e in entries]
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
-            scale: float) -> None:
+            scale: float, acc: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+        """Decode into ``out`` (and ``lse``).  With ``acc = (o_acc [S, H, D] in
+        q's dtype, lse_acc [H, S] float32)`` the accumulator is merged in by the
+        same launch (``hcp_decode_splitkv_acc``); ``out`` / ``lse`` may be the
+        accumulator's own tensors."""
         L = _lib.lib()
-        with torch.cuda.device(q.device):
-            rc = L.hcp_decode_splitkv(
-                q.data_ptr(), q.stride(0), q.stride(1),
-                self.entries_dev.data_ptr(), self.num_entries,
-                self.splits_dev.data_ptr(), self.num_splits,
-                self.starts_dev.data_ptr(), self.num_seqs,
-                self.workspace.data_ptr(), self.ws_bytes,
-                out.data_ptr(), out.stride(0), out.stride(1),
+        # fp32 partials: stream-ordered scratch from torch's caching allocator
+        workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=q.device)
+        head = (q.data_ptr(), q.stride(0), q.stride(1),
+                self.entries_ptr, self.num_entries,
+                self.splits_ptr, self.num_splits,
+                self.starts_ptr, self.num_seqs,
+                workspace.data_ptr(), self.ws_bytes)
+        tail = (out.data_ptr(), out.stride(0), out.stride(1),
                 lse.data_ptr() if lse is not None else None,
                 lse.stride(0) if lse is not None else 0,
                 self.num_heads, self.num_kv_heads, self.head_dim, float(scale),
-                _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
-            )
-        _lib.check(rc, "hcp_decode_splitkv")
+                _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+        with torch.cuda.device(q.device):
+            if acc is None:
+                rc = L.hcp_decode_splitkv(*head, *tail)
+                name = "hcp_decode_splitkv"
+            else:
+                ao, al = acc
+                if ao.dtype != q.dtype or tuple(ao.shape) != tuple(q.shape) or ao.stride(-1) != 1:
+                    raise ValueError("acc o must match q's dtype and shape, contiguous head_dim")
+                if al.dtype != torch.float32 or tuple(al.shape) != (q.shape[1], q.shape[0]) \
+                        or al.stride(1) != 1:
+                    raise ValueError("acc lse must be float32 [H, S], contiguous along S")
+                if not (ao.is_cuda and al.is_cuda):
+                    raise ValueError("accumulator must be on the GPU")
+                rc = L.hcp_decode_splitkv_acc(
+                    *head, ao.data_ptr(), ao.stride(0), ao.stride(1), al.data_ptr(),
+                    al.stride(0), *tail)
+                name = "hcp_decode_splitkv_acc"
+        _lib.check(rc, name)
 
 
 def decode_attn(
@@ -338,9 +378,11 @@ def decode_attn(
     out: torch.Tensor | None = None,
     with_lse: bool = False,
     split_tokens: int | None = None,
+    acc: tuple[torch.Tensor, torch.Tensor] | None = None,
 ):
     """Split-KV decode: q ``[S, H, D]`` (one token per sequence) over all
-    segments of each sequence, merged.  Returns out (and lse ``[H, S]``)."""
+    segments of each sequence, merged (and merged into ``acc`` when given).
+    Returns out (and lse ``[H, S]``)."""
     if q.dtype not in (torch.float16, torch.bfloat16) or q.stride(-1) != 1:
         raise ValueError("q must be float16/bfloat16 with contiguous head_dim")
     if len(segments) != q.shape[0]:
@@ -350,5 +392,5 @@ def decode_attn(
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
     lse = torch.empty((h, s), dtype=torch.float32, device=q.device) if with_lse else None
-    batch.run(q, out, lse, scale)
+    batch.run(q, out, lse, scale, acc)
     return (out, lse) if with_lse else out

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 3
+#define HCP_ABI_VERSION 4
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -210,6 +210,36 @@ int hcp_decode_splitkv(const void* q, int64_t q_stride_tok,
                        int64_t lse_stride_head, int32_t num_heads,
                        int32_t num_kv_heads, int32_t head_dim, float scale,
                        int32_t dtype, void* stream);
+
+/*
+ * Split-KV decode merged into a running accumulator: the decode ring's step
+ * on one node.  Replaces RingDecodeNode.handle_packet's partial over
+ * cat(chunk snapshot, growth) and _merge_pair (ring_decode.py:224-237,
+ * :46-61): the partials of every segment of sequence s and the accumulator
+ * row (acc_o [num_seqs, H, D] in `dtype`, acc_lse [H, num_seqs] float32) are
+ * merged in the second kernel -- no separate merge launch -- into `out` and,
+ * when `lse` is not NULL, the merged LSE.  An accumulator LSE of -inf (or
+ * +inf, read as empty as merge_attn_states does) contributes nothing.
+ * `out` may be `acc_o` and `lse` may be `acc_lse` (in-place update).  Other
+ * arguments as hcp_decode_splitkv.
+ */
+int hcp_decode_splitkv_acc(const void* q, int64_t q_stride_tok,
+                           int64_t q_stride_head,
+                           const hcp_varlen_entry* entries,
+                           int32_t num_entries,
+                           const hcp_decode_split* splits,
+                           int32_t num_splits,
+                           const int32_t* seq_partial_start,
+                           int32_t num_seqs, void* workspace,
+                           size_t workspace_bytes, const void* acc_o,
+                           int64_t acc_stride_tok, int64_t acc_stride_head,
+                           const float* acc_lse,
+                           int64_t acc_lse_stride_head, void* out,
+                           int64_t o_stride_tok, int64_t o_stride_head,
+                           float* lse, int64_t lse_stride_head,
+                           int32_t num_heads, int32_t num_kv_heads,
+                           int32_t head_dim, float scale, int32_t dtype,
+                           void* stream);
 
 /*
  * LSE merge of two partial attentions over disjoint key sets:

@@ -28,6 +28,16 @@ order, the reference's plain-PyTorch path of stark-sim/hcp-vllm-plugin:
   ring_backend.py:576-834 (non-decode-ring branch): vanilla causal when there is
   no peer, ``n_a`` queries inside the peer region, local causal at offset
   ``qpos0 + n_a - peer_end``, peer non-causal, merge, cast to ``output.dtype``.
+* ``ring_decode_hop``    <- one node's step ``RingDecodeNode.handle_packet``
+  ring_decode.py:187-239: partial over ``cat(chunk snapshot, growth)``
+  non-causal, then ``_merge_pair(o_acc, lse_acc, o_loc, lse_loc)``.
+* ``DecodeRingSim``      <- the memory-split decode protocol as a whole:
+  owner side ring_backend.py:643-722 (own chunk + owned growth + current
+  token causal at ``len-1``, growth assignment ``growth_assignee``
+  ring_decode.py:30-43, last step's token shipped on this step's packet with
+  ``growth_target = assignee + 1``) and every node's hop in ring order,
+  ring_decode.py:187-259 (growth appended only at its target, before the
+  partial).
 
 Semantics fixed by the reference (ring_triton_attn.py:1-26,64,95-108,137-140):
 q ``[Tq, H, D]``, k/v ``[Tk, Hkv, D]``, out ``[Tq, H, D]``, lse ``[H, Tq]`` float32
@@ -61,6 +71,8 @@ __all__ = [
     "gather_paged",
     "kv_cache_update",
     "ring_forward",
+    "ring_decode_hop",
+    "DecodeRingSim",
     "causal_pairs",
     "attn_flops",
 ]
@@ -323,6 +335,97 @@ def ring_forward(
             o_b = lse_merge(o_loc, lse_loc, o_peer, lse_peer)
             output[qs + n_a : qe] = o_b.to(out_dtype)
     return output
+
+
+def ring_decode_hop(
+    q: torch.Tensor,
+    o_acc: torch.Tensor,
+    lse_acc: torch.Tensor,
+    k_snap: torch.Tensor,
+    v_snap: torch.Tensor,
+    growth_k: torch.Tensor | None,
+    growth_v: torch.Tensor | None,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """One node's accumulator step (ring_decode.py:224-237), fp32.
+
+    ``k = cat(k_snap, growth_k)`` (:229-232), ``(o_loc, lse_loc)`` non-causal
+    over it (:234-236), then ``merge_pair(o_acc, lse_acc, o_loc, lse_loc)``
+    (:237).
+    """
+    k, v = k_snap.float(), v_snap.float()
+    if growth_k is not None:
+        k = torch.cat([k, growth_k.float()], dim=0)
+        v = torch.cat([v, growth_v.float()], dim=0)
+    o_loc, lse_loc = attn_with_lse(q.float(), k, v, scale, None)
+    return merge_pair(o_acc.float(), lse_acc.float(), o_loc, lse_loc)
+
+
+class DecodeRingSim:
+    """The memory-split decode protocol of one request, restated in fp32.
+
+    Ring order: transport index 0 is the owner, 1..N-1 the prefix peers
+    (growth index i -> transport i + 1; the owner's growth index is N - 1).
+    ``peer_chunks[i]`` is peer i's chunk snapshot ``(k, v)``; ``own_chunk`` the
+    owner's own chunk (its pool region ``[plen, plen + own_len)``).
+    ``step(q, k_cur, v_cur, pos)`` is one decode step of one layer:
+
+    * owner (ring_backend.py:652-689): ``assignee = growth_assignee(pos)``;
+      ``ship`` = the previous step's pending token; local partial over
+      ``own chunk + owned growth + current token`` (causal at ``len-1``: every
+      key visible); the current token joins the owned growth or becomes the
+      pending token;
+    * the packet visits peers 1..N-1 in order (ring_decode.py:187-259): a node
+      appends shipped growth when it is the target, then merges its partial
+      over ``snapshot + its growth`` into the accumulator.
+
+    Returns the final (O, LSE) the owner receives, plus the growth held by
+    every ring member (``growth_of[i]`` for transport index i).
+    """
+
+    def __init__(self, peer_chunks, own_chunk, scale: float, policy: str = "rr"):
+        self.peer_chunks = [(k.float(), v.float()) for k, v in peer_chunks]
+        self.own_k, self.own_v = own_chunk[0].float(), own_chunk[1].float()
+        self.scale = scale
+        self.policy = policy
+        self.n = len(peer_chunks) + 1
+        self.growth_of: list[list[tuple[torch.Tensor, torch.Tensor]]] = [
+            [] for _ in range(self.n)]
+        self.pending = None
+
+    def assignee(self, pos: int) -> int:
+        """ring_decode.py:30-43 (growth index)."""
+        return self.n - 1 if self.policy == "owner" else pos % self.n
+
+    @staticmethod
+    def _cat(base_k, base_v, extra):
+        ks = [base_k] + [k for k, _ in extra]
+        vs = [base_v] + [v for _, v in extra]
+        return torch.cat(ks, 0), torch.cat(vs, 0)
+
+    def step(self, q, k_cur, v_cur, pos: int):
+        q, k_cur, v_cur = q.float(), k_cur.float(), v_cur.float()
+        a = self.assignee(pos)
+        ship, self.pending = self.pending, None
+        owner_t = 0
+        k_loc, v_loc = self._cat(self.own_k, self.own_v,
+                                 self.growth_of[owner_t] + [(k_cur, v_cur)])
+        o, lse = attn_with_lse(q, k_loc, v_loc, self.scale, k_loc.shape[0] - 1)
+        if a == self.n - 1:
+            self.growth_of[owner_t].append((k_cur, v_cur))
+        else:
+            self.pending = (a + 1, k_cur, v_cur)
+        for t in range(1, self.n):
+            if ship is not None and ship[0] == t:
+                self.growth_of[t].append((ship[1], ship[2]))
+                ship = None
+            ck, cv = self.peer_chunks[t - 1]
+            gk = gv = None
+            if self.growth_of[t]:
+                gk = torch.cat([k for k, _ in self.growth_of[t]], 0)
+                gv = torch.cat([v for _, v in self.growth_of[t]], 0)
+            o, lse = ring_decode_hop(q, o, lse, ck, cv, gk, gv, self.scale)
+        return o, lse
 
 
 def causal_pairs(tq: int, tk: int, offset: int | None) -> int:

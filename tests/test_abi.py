@@ -209,6 +209,28 @@ def test_argument_validation_status_codes(L):
     assert rc == _lib.HCP_EUNSUPPORTED  # head_dim 12
 
 
+def _dec_acc(L, **kw):
+    a = dict(q=16, acc_o=16, acc_lse=16, out=16, h=28, hkv=4, d=128, seqs=1, scale=0.1,
+             dtype=_lib.DTYPE_BF16)
+    a.update(kw)
+    return L.hcp_decode_splitkv_acc(a["q"], 4096, 128, None, 0, None, 0, 16, a["seqs"], None, 0,
+                                    a["acc_o"], 4096, 128, a["acc_lse"], 1, a["out"], 4096, 128,
+                                    None, 0, a["h"], a["hkv"], a["d"], a["scale"], a["dtype"],
+                                    None)
+
+
+def test_decode_splitkv_acc_status_codes(L):
+    """Argument checks of the accumulator decode, all returned before any launch."""
+    assert _dec_acc(L, acc_o=None) == _lib.HCP_EINVAL
+    assert b"null accumulator" in L.hcp_last_error()
+    assert _dec_acc(L, acc_lse=None) == _lib.HCP_EINVAL
+    assert _dec_acc(L, acc_o=17) == _lib.HCP_EINVAL       # odd address
+    assert _dec_acc(L, d=96) == _lib.HCP_EUNSUPPORTED
+    assert _dec_acc(L, h=30) == _lib.HCP_EINVAL           # not a multiple of hkv
+    assert _dec_acc(L, scale=0.0) == _lib.HCP_EINVAL
+    assert _dec_acc(L, seqs=0) == _lib.HCP_OK              # nothing to do, nothing launched
+
+
 def _cache_desc(bs=16, nb=4):
     c = _lib.PagedCacheDesc()
     c.k_addr, c.v_addr = 0x1000, 0x1100

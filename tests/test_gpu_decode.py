@@ -82,3 +82,78 @@ def test_decode_empty_sequence(dev):
     assert torch.all(out[1] == 0) and torch.all(torch.isneginf(lse[:, 1]))
     ro, rl = orc.attn_with_lse(q[:1].float().cpu(), k.float().cpu(), k.float().cpu(), 0.088, None)
     assert max_err(out[:1], ro) <= OUT_TOL[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# hcp_decode_splitkv_acc: the decode merged into a running accumulator
+# ---------------------------------------------------------------------------
+def _acc_case(dev, dtype, seg_lens, split, seed, in_place=False, acc_lse_fill=None):
+    h, hkv, d = 28, 4, 128
+    gen = torch.Generator().manual_seed(seed)
+    s = len(seg_lens)
+    q = randn(gen, (s, h, d), dtype)
+    o_acc = randn(gen, (s, h, d), dtype)
+    l_acc = torch.randn(h, s, generator=gen) * 4
+    if acc_lse_fill is not None:
+        l_acc[:, 0] = acc_lse_fill
+    ks = [[randn(gen, (n, hkv, d), dtype) for n in lens] for lens in seg_lens]
+    vs = [[randn(gen, (n, hkv, d), dtype) for n in lens] for lens in seg_lens]
+    kd = [[k.to(dev) for k in row] for row in ks]
+    vd = [[v.to(dev) for v in row] for row in vs]
+    segs = [[segment_contiguous(k, v) for k, v in zip(kr, vr)] for kr, vr in zip(kd, vd)]
+    qd, oad, lad = q.to(dev), o_acc.to(dev), l_acc.to(dev)
+    scale = scale_for(d)
+    if in_place:
+        decode_attn(qd, segs, hkv, scale, out=oad, split_tokens=split, acc=(oad, lad))
+        # lse in place: run again through the batch API with lse = acc lse
+        out, lse = oad, None
+    else:
+        out, lse = decode_attn(qd, segs, hkv, scale, with_lse=True, split_tokens=split,
+                               acc=(oad, lad))
+    torch.cuda.synchronize()
+    for r in range(s):
+        ro, rl = o_acc[r:r + 1].float(), l_acc[:, r:r + 1].clone()
+        rl[torch.isposinf(rl)] = float("-inf")
+        for k, v in zip(ks[r], vs[r]):
+            if k.shape[0] == 0:
+                continue
+            po, pl = orc.attn_with_lse(q[r:r + 1].float(), k.float(), v.float(), scale, None)
+            ro, rl = orc.merge_pair(ro, rl, po, pl)
+        assert max_err(out[r:r + 1], ro) <= OUT_TOL[dtype], r
+        if lse is not None:
+            assert max_err(lse[:, r:r + 1], rl) <= LSE_TOL, r
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("split", [None, 64, 100 * 64])
+def test_decode_acc_vs_oracle(dev, dtype, split):
+    """Chunk + growth segments of several lengths; split 64 gives one
+    sequence 500+ partials, exercising the reduce's 8-wide batches and its
+    remainder."""
+    _acc_case(dev, dtype, [[32768, 512], [1000, 3], [1, 0], [700]], split, seed=61)
+
+
+def test_decode_acc_empty_accumulator_and_no_keys(dev):
+    """An accumulator LSE of -inf or +inf contributes nothing; a sequence with
+    no keys returns the accumulator itself."""
+    _acc_case(dev, torch.bfloat16, [[300], [0]], None, seed=62, acc_lse_fill=float("-inf"))
+    _acc_case(dev, torch.bfloat16, [[300], [0]], None, seed=63, acc_lse_fill=float("inf"))
+
+
+def test_decode_acc_in_place(dev):
+    """out may be the accumulator's own O (and lse its LSE)."""
+    _acc_case(dev, torch.float16, [[5000, 17], [64]], 256, seed=64, in_place=True)
+    h, hkv, d = 28, 4, 128
+    gen = torch.Generator().manual_seed(65)
+    q = randn(gen, (1, h, d), torch.bfloat16).to(dev)
+    k = randn(gen, (2000, hkv, d), torch.bfloat16).to(dev)
+    v = randn(gen, (2000, hkv, d), torch.bfloat16).to(dev)
+    o = randn(gen, (1, h, d), torch.bfloat16).to(dev)
+    lse = (torch.randn(h, 1, generator=gen) * 2).to(dev)
+    want_o, want_l = decode_attn(q, [[segment_contiguous(k, v)]], hkv, 0.088, with_lse=True,
+                                 acc=(o, lse))
+    from hcp_vllm_plugin_amd.varlen import DecodeBatch
+
+    DecodeBatch([[segment_contiguous(k, v)]], h, hkv, d, dev).run(q, o, lse, 0.088, acc=(o, lse))
+    torch.cuda.synchronize()
+    assert torch.equal(o, want_o) and torch.equal(lse, want_l)

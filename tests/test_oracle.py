@@ -321,3 +321,91 @@ def test_causal_pairs_and_flops():
     # C2: 8192 local causal (frame offset 0) + 8192 peer keys, 7B shape
     f = orc.attn_flops(28, 128, orc.causal_pairs(8192, 8192, 0) + 8192 * 8192)
     assert abs(f / 1e12 - 1.4432) < 1e-3
+
+
+# ---------------------------------------------------------------------------
+# Decode ring (ring_decode.py:187-259, ring_backend.py:643-722)
+# ---------------------------------------------------------------------------
+def _brute_t(q, k, v, scale, off):
+    o, lse = brute(q, k, v, scale, off)
+    return torch.from_numpy(o), torch.from_numpy(lse)
+
+
+def test_ring_decode_hop_from_empty_accumulator_is_plain_attention():
+    """An empty accumulator (o = 0, lse = -inf) merged with one hop is the
+    float64 brute-force attention over snapshot + growth."""
+    g = torch.Generator().manual_seed(81)
+    q = rnd(g, 1, 4, 16)
+    ck, cv = rnd(g, 11, 2, 16), rnd(g, 11, 2, 16)
+    gk, gv = rnd(g, 3, 2, 16), rnd(g, 3, 2, 16)
+    o0 = torch.zeros(1, 4, 16)
+    l0 = torch.full((4, 1), float("-inf"))
+    o, lse = orc.ring_decode_hop(q, o0, l0, ck, cv, gk, gv, 0.25)
+    bo, bl = _brute_t(q, torch.cat([ck, gk]), torch.cat([cv, gv]), 0.25, None)
+    assert (o.double() - bo).abs().max() < 1e-5
+    assert (lse.double() - bl).abs().max() < 1e-5
+    # without growth the hop sees the snapshot alone
+    o, lse = orc.ring_decode_hop(q, o0, l0, ck, cv, None, None, 0.25)
+    bo, bl = _brute_t(q, ck, cv, 0.25, None)
+    assert (o.double() - bo).abs().max() < 1e-5
+
+
+@pytest.mark.parametrize("n,policy", [(2, "rr"), (3, "rr"), (4, "rr"), (3, "owner")])
+def test_decode_ring_protocol_equals_full_attention(n, policy):
+    """Memory-split decode is exact: after every step the accumulator the
+    owner gets back is attention over ALL keys (every prefix chunk, the own
+    chunk and every decode token so far, including the one-step-late growth),
+    and each peer holds exactly the positions assigned to it."""
+    g = torch.Generator().manual_seed(90 + n)
+    H, HKV, D, scale = 4, 2, 16, 0.25
+    peers = [(rnd(g, 5 + 3 * i, HKV, D), rnd(g, 5 + 3 * i, HKV, D)) for i in range(n - 1)]
+    own = (rnd(g, 6, HKV, D), rnd(g, 6, HKV, D))
+    sim = orc.DecodeRingSim(peers, own, scale, policy)
+    allk = [k for k, _ in peers] + [own[0]]
+    allv = [v for _, v in peers] + [own[1]]
+    pos0 = sum(k.shape[0] for k in allk)
+    for t in range(3 * n + 2):
+        q = rnd(g, 1, H, D)
+        kc, vc = rnd(g, 1, HKV, D), rnd(g, 1, HKV, D)
+        allk.append(kc)
+        allv.append(vc)
+        o, lse = sim.step(q, kc, vc, pos0 + t)
+        bo, bl = _brute_t(q, torch.cat(allk), torch.cat(allv), scale, None)
+        assert (o.double() - bo).abs().max() < 1e-5, t
+        assert (lse.double() - bl).abs().max() < 1e-5, t
+    # growth placement: position p lives on growth index p % n (rr) or the
+    # owner; the last step's token is still pending when it belongs to a peer
+    last = pos0 + 3 * n + 1
+    for tidx in range(n):
+        gi = n - 1 if tidx == 0 else tidx - 1
+        want = [p for p in range(pos0, last + 1) if sim.assignee(p) == gi]
+        if tidx != 0 and sim.assignee(last) == gi:
+            want = want[:-1]
+        assert len(sim.growth_of[tidx]) == len(want), (tidx, want)
+
+
+def test_decode_ring_sim_catches_a_lost_shipment():
+    """A planted mistake (the pending token is never shipped) breaks the
+    full-attention check above -- the check has teeth."""
+    g = torch.Generator().manual_seed(97)
+    H, HKV, D, scale = 4, 2, 16, 0.25
+    peers = [(rnd(g, 4, HKV, D), rnd(g, 4, HKV, D))]
+    own = (rnd(g, 4, HKV, D), rnd(g, 4, HKV, D))
+
+    class Lossy(orc.DecodeRingSim):
+        def step(self, q, k_cur, v_cur, pos):
+            self.pending = None
+            return super().step(q, k_cur, v_cur, pos)
+
+    sim = Lossy(peers, own, scale, "rr")
+    allk, allv = [peers[0][0], own[0]], [peers[0][1], own[1]]
+    worst = 0.0
+    for t in range(4):
+        q = rnd(g, 1, H, D)
+        kc, vc = rnd(g, 1, HKV, D), rnd(g, 1, HKV, D)
+        allk.append(kc)
+        allv.append(vc)
+        o, _ = sim.step(q, kc, vc, 8 + t)
+        bo, _ = _brute_t(q, torch.cat(allk), torch.cat(allv), scale, None)
+        worst = max(worst, (o.double() - bo).abs().max().item())
+    assert worst > 1e-3
