@@ -342,6 +342,26 @@ def bench_peer_ingest(dev, steps, warmup, chunks=(4096, 4096), fmt="k_v"):
     }
 
 
+def bench_sliding_window(dev, steps, warmup, window=4096, n=8192):
+    """The local causal pass of the 8k step with a sliding window (a
+    Mistral-style 4096-key window at the 7B attention shape): the kernel
+    skips keys below each workgroup's window, so the algorithmic work is the
+    visible pairs sum_i min(i + 1, window)."""
+    from hcp_vllm_plugin_amd import ring_attn_with_lse
+
+    q, kl, vl, _, _ = prefill_inputs(dev)
+    ms = timed(lambda: ring_attn_with_lse(q, kl, vl, SCALE, 0, window), steps, warmup)
+    pairs = sum(min(i + 1, window) for i in range(n))
+    flops = 4 * D * H * pairs
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "workload": (f"local causal pass, {n} queries x {n} keys, sliding window {window}, "
+                     f"28/4 heads, head_dim 128, bf16"),
+        "ms": round(ms, 4), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+        "tflop": round(flops / 1e12, 3),
+    }
+
+
 def bench_ring_decode_hop(dev, steps, warmup, seed=6, chunk=32768, growth=512):
     """One decode-ring hop at Qwen2.5-7B shape (q [1,28,128] bf16): a node's
     partial over its 32768-key chunk snapshot + 512 growth tokens merged into
@@ -546,7 +566,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
-                                       "kvwrite", "ingest", "ringdec", "copy"),
+                                       "kvwrite", "ingest", "ringdec", "window", "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -573,6 +593,9 @@ def main():
     if args.part == "ingest":
         print(json.dumps(bench_peer_ingest(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "window":
+        print(json.dumps(bench_sliding_window(dev, args.steps, args.warmup)), flush=True)
+        return
     if args.part == "ringdec":
         print(json.dumps(bench_ring_decode_hop(dev, args.steps, args.warmup)), flush=True)
         return
@@ -594,6 +617,7 @@ def main():
         extra["kv_cache_write"] = bench_kv_cache_write(dev, args.steps, args.warmup)
         extra["peer_ingest"] = bench_peer_ingest(dev, args.steps, args.warmup)
         extra["ring_decode_hop"] = bench_ring_decode_hop(dev, args.steps, args.warmup)
+        extra["sliding_window"] = bench_sliding_window(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 

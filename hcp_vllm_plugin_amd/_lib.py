@@ -56,7 +56,7 @@ EXPORTED_SYMBOLS = (
     "hcp_reshape_and_cache",
 )
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class KvSegment(ctypes.Structure):
@@ -131,7 +131,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_attn_fwd_lse.argtypes = [
         _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32,
         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-        _F, _I32, _I64, _I32, _P,
+        _F, _I32, _I64, _I32, _I32, _P,
     ]
     lib.hcp_varlen_block_m.restype = ctypes.c_int
     lib.hcp_varlen_block_m.argtypes = [_I32, _I32]
@@ -140,7 +140,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_attn_fwd_varlen.restype = ctypes.c_int
     lib.hcp_attn_fwd_varlen.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
-        _P, _I32, _P, _I32, _I32, _I32, _I32, _F, _I32, _I32, _I32, _P,
+        _P, _I32, _P, _I32, _I32, _I32, _I32, _F, _I32, _I32, _I32, _I32, _P,
     ]
     lib.hcp_plan_decode_splits.restype = ctypes.c_int
     lib.hcp_plan_decode_splits.argtypes = [_P, _I32, _P, _I32, _I32, _I32, _P, _I32, _P]

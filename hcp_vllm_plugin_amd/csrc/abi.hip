@@ -73,7 +73,7 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, flo
                      int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
                      int64_t v_stride_head, int64_t o_stride_tok, int64_t o_stride_head,
                      int64_t lse_stride_head, float scale, int32_t causal,
-                     int64_t causal_offset, int32_t dtype, void* stream) {
+                     int64_t causal_offset, int32_t window, int32_t dtype, void* stream) {
   const char* who = "hcp_attn_fwd_lse";
   int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
   if (rc) return rc;
@@ -89,6 +89,7 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, flo
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(HCP_EINVAL, "%s: scale must be finite and > 0", who);
   if (tq > (int64_t)INT32_MAX * 64) return fail(HCP_EINVAL, "%s: tq too large", who);
+  if (window < 0) return fail(HCP_EINVAL, "%s: negative window", who);
 
   hcp::FwdParams p{};
   p.q = q;
@@ -107,6 +108,7 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, flo
   p.single.q_start = 0;
   p.single.q_len = tq;
   p.single.causal_offset = causal ? causal_offset : 0;
+  p.window = causal ? window : 0;
   p.single.kv.k_addr = reinterpret_cast<uint64_t>(k);
   p.single.kv.v_addr = reinterpret_cast<uint64_t>(v);
   p.single.kv.stride_tok = k_stride_tok;
@@ -168,7 +170,8 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                         int64_t lse_stride_head, const hcp_varlen_entry* entries,
                         int32_t num_entries, const int32_t* tiles, int32_t num_tiles,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
-                        int32_t causal, int32_t paged, int32_t dtype, void* stream) {
+                        int32_t causal, int32_t window, int32_t paged, int32_t dtype,
+                        void* stream) {
   const char* who = "hcp_attn_fwd_varlen";
   int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
   if (rc) return rc;
@@ -180,7 +183,9 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     return fail(HCP_EINVAL, "%s: strides must be multiples of 8 elements", who);
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(HCP_EINVAL, "%s: scale must be finite and > 0", who);
+  if (window < 0) return fail(HCP_EINVAL, "%s: negative window", who);
   hcp::FwdParams p{};
+  p.window = causal ? window : 0;
   p.q = q;
   p.q_stride_tok = q_stride_tok;
   p.q_stride_head = q_stride_head;

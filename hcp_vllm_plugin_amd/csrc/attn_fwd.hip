@@ -150,6 +150,20 @@ fa_fwd_kernel(FwdParams p) {
     e = p.single;
     qb = CAUSAL ? (p.num_tiles - 1 - tile) : tile;  // heaviest first
   }
+  // Sliding window (causal only): row i sees keys (off + i - window, off + i].
+  // The workgroup's first row has the lowest bound, so the segment is rebased
+  // to it: keys below are never loaded, and rows whose bound is higher mask
+  // the boundary tiles.
+  const int64_t win = CAUSAL ? p.window : 0;
+  if (win > 0) {
+    int64_t lo = e.causal_offset + static_cast<int64_t>(qb) * BM - win + 1;
+    if (lo > 0) {
+      if (lo > e.kv.len) lo = e.kv.len;
+      e.kv.start += lo;
+      e.kv.len -= lo;
+      e.causal_offset -= lo;
+    }
+  }
   const int64_t q_len = e.q_len;
   const int kv_len = static_cast<int>(e.kv.len);
   const int64_t off = e.causal_offset;
@@ -350,9 +364,12 @@ fa_fwd_kernel(FwdParams p) {
   };
 
   // causal diagonal / ragged masking of tile n (keys n*BN ..): -inf
+  // (and, with a window, tiles below some row's lower bound: the wave's last
+  // row has the highest bound off + wave_q0 + 32 - window)
   auto needs_mask = [&](int n) __attribute__((always_inline)) {
     const int n0 = n * BN;
-    return (n0 + BN > kv_len) || (CAUSAL && (n0 + BN - 1 > off + wave_q0));
+    return (n0 + BN > kv_len) || (CAUSAL && (n0 + BN - 1 > off + wave_q0)) ||
+           (win > 0 && n0 < off + wave_q0 + 32 - win);
   };
   auto apply_mask = [&](f32x16 (&S)[2], int n) __attribute__((always_inline)) {
     const int n0 = n * BN;
@@ -360,12 +377,15 @@ fa_fwd_kernel(FwdParams p) {
     const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
     const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
     const int lim = lim_r < lim_c ? lim_r : lim_c;
+    // lowest visible key of the lane's row, relative to the tile
+    const int64_t lo64 = win > 0 ? off + qi - win + 1 - n0 : 0;
+    const int lo = lo64 > 0 ? (lo64 < BN ? static_cast<int>(lo64) : BN) : 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kk = 32 * h + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (kk > lim) S[h][r] = -INFINITY;
+        if (kk > lim || kk < lo) S[h][r] = -INFINITY;
       }
   };
 

@@ -22,6 +22,7 @@ struct FwdParams {
   int32_t num_tiles;                // varlen: tiles; else query blocks
   int32_t num_heads, num_kv_heads, group;
   float scale_log2;
+  int32_t window;           // causal only: key j visible iff j > qpos - window (0: none)
   hcp_varlen_entry single;  // non-varlen: the one entry
 };
 

@@ -51,15 +51,21 @@ def ring_attn_with_lse(
     v: torch.Tensor,
     scale: float,
     causal_offset: int | None,
+    window: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Flash-style attention with LSE output (HIP, gfx950).
 
     causal_offset: absolute position of query token 0 within the KV range
-    (None => non-causal, all keys visible).  Returns (out ``[Tq, H, D]`` in
-    q.dtype, lse ``[H, Tq]`` float32 natural log).  A query with no visible
-    key (empty KV, or a negative offset) gets out 0 and lse -inf.
+    (None => non-causal, all keys visible).  window: sliding window on the
+    causal pass as ``_attn_with_lse`` applies it (ring_backend.py:372,
+    397-398): query i at p = causal_offset + i sees keys p - window < j <= p;
+    ignored when non-causal.  Returns (out ``[Tq, H, D]`` in q.dtype, lse
+    ``[H, Tq]`` float32 natural log).  A query with no visible key (empty KV,
+    or a negative offset) gets out 0 and lse -inf.
     """
     check_qkv(q, k, v)
+    if window is not None and window <= 0:
+        raise ValueError("window must be a positive number of keys")
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     tq, num_heads, head_dim = q.shape
     tk, num_kv_heads = k.shape[0], k.shape[1]
@@ -79,6 +85,7 @@ def ring_attn_with_lse(
             v.stride(0), v.stride(1), out.stride(0), out.stride(1), lse.stride(0),
             float(scale), 0 if causal_offset is None else 1,
             0 if causal_offset is None else int(causal_offset),
+            0 if (window is None or causal_offset is None) else int(window),
             _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
         )
     _lib.check(rc, "hcp_attn_fwd_lse")

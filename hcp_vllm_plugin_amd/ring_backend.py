@@ -60,6 +60,8 @@ from .varlen import (
     make_entry,
     segment_contiguous,
     segment_paged,
+    trim_segment,
+    window_tail,
 )
 
 logger = logging.getLogger(__name__)
@@ -281,14 +283,14 @@ def _attn(
     q_pos0_in_kv: int | None,
     window: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Attention + LSE on the HIP kernel (ring_backend.py:309-336 contract).
+    """Attention + LSE on the HIP kernel (ring_backend.py:309-336 contract),
+    sliding window included (the reference sends windowed calls to its torch
+    path, :323,336; here the kernel applies it).
 
     Returns (out ``[Tq, H, D]`` in q.dtype, lse ``[H, Tq]`` float32).
     """
     _require_fast("HCP_RING_IMPL", _ring_impl())
-    if window is not None:
-        raise NotImplementedError("sliding-window attention is not built for the HIP path")
-    o, lse = ring_attn_with_lse(q, k, v, scale, q_pos0_in_kv)
+    o, lse = ring_attn_with_lse(q, k, v, scale, q_pos0_in_kv, window)
     _count("attn")
     return o, lse
 
@@ -378,11 +380,13 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
             raise NotImplementedError("HCP ring backend: ALiBi not supported")
         if logits_soft_cap:
             raise NotImplementedError("HCP ring backend: soft cap not supported")
-        if sliding_window is not None:
-            raise NotImplementedError("HCP ring backend (HIP): sliding window not supported")
+        if sliding_window is not None and int(sliding_window) <= 0:
+            raise ValueError("sliding_window must be a positive number of keys")
         if kv_cache_dtype not in ("auto", "float16", "bfloat16"):
             raise NotImplementedError(f"kv_cache_dtype {kv_cache_dtype} not supported")
-        self.sliding_window = sliding_window
+        # applied to every causal pass (local segments), never to the
+        # non-causal peer pass -- ring_backend.py:490-492,786,815,826-830
+        self.sliding_window = int(sliding_window) if sliding_window is not None else None
         self.num_queries_per_kv = self.num_heads // self.num_kv_heads
 
     # -- paged KV write (the step before the path) ----------------------------
@@ -583,10 +587,13 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
             own = segment_paged(pc, row, plen, own_len) if own_len > 0 else None
             if assignee == dr["own_index"]:
                 g.append(k_cur, v_cur)
-                segs[r] = [own, g.segment()]
+                local = [own, g.segment()]
             else:
-                segs[r] = [own, g.segment(), segment_contiguous(k_cur, v_cur)]
+                local = [own, g.segment(), segment_contiguous(k_cur, v_cur)]
                 dr["pending_growth"][layer_name] = (assignee, k_cur, v_cur)
+            # causal at len - 1 over the concatenation (:672-679): every key,
+            # or the last `sliding_window` of them
+            segs[r] = window_tail(local, self.sliding_window)
         return segs
 
     def _local_partial(self, q_r, segs):
@@ -620,13 +627,13 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         if not plan.any_peer:
             lse = torch.empty((h, query.shape[0]), dtype=torch.float32, device=dev)
             VarlenLaunch(plan.local, True, True, dev).run(query, out, lse, self.num_kv_heads,
-                                                         self.scale)
+                                                         self.scale, self.sliding_window)
             _count("attn")
             return
         o_loc = torch.empty_like(query, memory_format=torch.contiguous_format)
         lse_loc = torch.full((h, query.shape[0]), float("-inf"), dtype=torch.float32, device=dev)
         VarlenLaunch(plan.local, True, True, dev).run(query, o_loc, lse_loc, self.num_kv_heads,
-                                                     self.scale)
+                                                     self.scale, self.sliding_window)
         _count("attn")
         o_peer = lse_peer = None
         for rnd in plan.peer_rounds:
@@ -653,8 +660,12 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         """One split-KV launch for the whole decode batch; decode-ring rows
         get their owner-local partial (with LSE) from the same launch."""
         segs: list[list] = [[] for _ in range(n)]
+        w = self.sliding_window
         for e in plan.local:
-            segs[e.q_start].append(e.kv)
+            kv = e.kv
+            if w is not None:  # the causal local pass sees keys (off - w, off]
+                kv = trim_segment(kv, min(kv.len, max(0, e.causal_offset - w + 1)))
+            segs[e.q_start].append(kv)
         for rnd in plan.peer_rounds:
             for kind in ("contig", "paged"):
                 for e in rnd[kind]:

@@ -145,6 +145,36 @@ def segment_paged(pc: PagedCache, block_table_row: torch.Tensor, start: int,
     return s
 
 
+def trim_segment(seg: KvSegment, skip: int) -> KvSegment:
+    """The same keys without the first ``skip`` (0 <= skip <= len)."""
+    if not 0 <= skip <= seg.len:
+        raise ValueError("trim beyond the segment")
+    s = KvSegment()
+    ctypes.memmove(ctypes.addressof(s), ctypes.addressof(seg), ctypes.sizeof(KvSegment))
+    s.start = seg.start + skip
+    s.len = seg.len - skip
+    s._keep = getattr(seg, "_keep", None)
+    return s
+
+
+def window_tail(segments: list, window: int | None) -> list:
+    """The last ``window`` keys of the concatenation of ``segments`` (in
+    order): what a query at the last position sees under a sliding window
+    (ring_backend.py:397-398 with qpos = len - 1).  None keeps all keys."""
+    segs = [s for s in segments if s is not None and s.len > 0]
+    if window is None:
+        return segs
+    if window <= 0:
+        raise ValueError("window must be a positive number of keys")
+    out, need = [], window
+    for s in reversed(segs):
+        if need == 0:
+            break
+        out.append(s if s.len <= need else trim_segment(s, s.len - need))
+        need -= min(need, s.len)
+    return out[::-1]
+
+
 def make_entry(q_start: int, q_len: int, seg: KvSegment, causal_offset: int = 0) -> VarlenEntry:
     e = VarlenEntry()
     e.q_start = q_start
@@ -222,9 +252,13 @@ class VarlenLaunch:
         self._keep = [getattr(e, "_keep", None) for e in entries]
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
-            num_kv_heads: int, scale: float) -> None:
+            num_kv_heads: int, scale: float, window: int | None = None) -> None:
+        """``window``: sliding window of a causal launch (query at p sees keys
+        p - window < j <= p in its entry's frame); ignored when non-causal."""
         if self.num_tiles == 0:
             return
+        if window is not None and window <= 0:
+            raise ValueError("window must be a positive number of keys")
         num_heads, head_dim = q.shape[1], q.shape[2]
         L = _lib.lib()
         with torch.cuda.device(q.device):
@@ -235,8 +269,8 @@ class VarlenLaunch:
                 self.entries_ptr, self.num_entries,
                 self.tiles_ptr, self.num_tiles,
                 num_heads, num_kv_heads, head_dim, float(scale),
-                int(self.causal), int(self.paged), _lib.dtype_code(q.dtype),
-                _lib.stream_ptr(q.device),
+                int(self.causal), int(window or 0) if self.causal else 0, int(self.paged),
+                _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
             )
         _lib.check(rc, "hcp_attn_fwd_varlen")
 
@@ -249,9 +283,11 @@ def varlen_attn_with_lse(
     scale: float,
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
+    window: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """One launch over all entries.  Rows not covered by an entry are left as
-    given (``out``/``lse`` allocated here start as 0 / -inf)."""
+    given (``out``/``lse`` allocated here start as 0 / -inf).  ``window``: as
+    ``VarlenLaunch.run``."""
     if q.dtype not in (torch.float16, torch.bfloat16) or q.stride(-1) != 1:
         raise ValueError("q must be float16/bfloat16 with contiguous head_dim")
     paged = bool(entries) and entries[0].kv.block_table != 0
@@ -260,7 +296,7 @@ def varlen_attn_with_lse(
     if lse is None:
         lse = torch.full((q.shape[1], q.shape[0]), float("-inf"), dtype=torch.float32,
                          device=q.device)
-    VarlenLaunch(entries, causal, paged, q.device).run(q, out, lse, num_kv_heads, scale)
+    VarlenLaunch(entries, causal, paged, q.device).run(q, out, lse, num_kv_heads, scale, window)
     return out, lse
 
 

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 4
+#define HCP_ABI_VERSION 5
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -115,6 +115,11 @@ const char* hcp_last_error(void);
  * hcp_vllm_plugin/ring_triton_attn.py:155-207 (and the torch fallback
  * _attn_with_lse, ring_backend.py:366-406).  causal = 0 is the peer
  * (non-causal) pass; causal = 1 with causal_offset is the local pass.
+ * window > 0 (causal only, ignored otherwise): sliding window of
+ * _attn_with_lse's `window` (ring_backend.py:372,397-398) -- query i at
+ * position p = causal_offset + i sees keys j with p - window < j <= p; the
+ * reference's Triton path has no window and falls back to torch for it
+ * (:315-323).  window = 0: none.
  * dtype: HCP_DTYPE_F16 or HCP_DTYPE_BF16 for q/k/v/out.  head_dim 64 or 128.
  */
 int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
@@ -125,7 +130,8 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
                      int64_t v_stride_tok, int64_t v_stride_head,
                      int64_t o_stride_tok, int64_t o_stride_head,
                      int64_t lse_stride_head, float scale, int32_t causal,
-                     int64_t causal_offset, int32_t dtype, void* stream);
+                     int64_t causal_offset, int32_t window, int32_t dtype,
+                     void* stream);
 
 /*
  * Query-block size (rows per tile) used by the varlen prefill kernel for this
@@ -151,7 +157,8 @@ int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries,
  * calls ring_attn_with_lse once per request and segment (:820-830).  The
  * paged form reads blocks in place, with no gather copy.  `entries` and
  * `tiles` are DEVICE arrays (tiles from hcp_plan_varlen_tiles).  All entries
- * of one launch share `causal` and the KV form (all paged or all contiguous,
+ * of one launch share `causal`, `window` (as hcp_attn_fwd_lse, relative to
+ * each entry's causal_offset) and the KV form (all paged or all contiguous,
  * `paged`).  out/lse rows are the entries' q rows.
  */
 int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok,
@@ -162,7 +169,8 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok,
                         const int32_t* tiles, int32_t num_tiles,
                         int32_t num_heads, int32_t num_kv_heads,
                         int32_t head_dim, float scale, int32_t causal,
-                        int32_t paged, int32_t dtype, void* stream);
+                        int32_t window, int32_t paged, int32_t dtype,
+                        void* stream);
 
 /*
  * Host-side split planner for hcp_decode_splitkv.  Each entry is one query

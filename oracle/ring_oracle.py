@@ -277,6 +277,7 @@ def ring_forward(
     peers: list[tuple[torch.Tensor, torch.Tensor] | None] | None = None,
     split_tokens: int = 0,
     out_dtype: torch.dtype | None = None,
+    window: int | None = None,
 ) -> torch.Tensor:
     """Restated segmentation of ``HcpRingAttentionImpl.forward``.
 
@@ -294,7 +295,9 @@ def ring_forward(
       all local KV (:811-817);
     * the rest: local causal on ``k_all[peer_end:]`` at offset
       ``qpos0 + n_a - peer_end`` (:820-827), peer non-causal (:828-830),
-      merged (:831), cast to the output dtype (:832).
+      merged (:831), cast to the output dtype (:832);
+    * ``window`` (``self.sliding_window``) goes to every causal call
+      (:786, :815, :826), never to the non-causal peer call (:828-830).
     """
     out_dtype = out_dtype or query.dtype
     output = torch.zeros(query.shape, dtype=out_dtype)
@@ -318,18 +321,18 @@ def ring_forward(
             peer_end = 0
             k_peer = v_peer = None
         if peer_end == 0:
-            o, _ = attn_with_lse(q_r, k_all, v_all, scale, qpos0)
+            o, _ = attn_with_lse(q_r, k_all, v_all, scale, qpos0, window)
             output[qs:qe] = o.to(out_dtype)
             continue
         n_a = max(0, min(tq, peer_end - qpos0))
         if n_a > 0:
-            o_a, _ = attn_with_lse(q_r[:n_a], k_all, v_all, scale, qpos0)
+            o_a, _ = attn_with_lse(q_r[:n_a], k_all, v_all, scale, qpos0, window)
             output[qs : qs + n_a] = o_a.to(out_dtype)
         if n_a < tq:
             q_b = q_r[n_a:]
             o_loc, lse_loc = attn_with_lse(
                 q_b, k_all[peer_end:], v_all[peer_end:], scale,
-                qpos0 + n_a - peer_end,
+                qpos0 + n_a - peer_end, window,
             )
             o_peer, lse_peer = attn_with_lse(q_b, k_peer, v_peer, scale, None)
             o_b = lse_merge(o_loc, lse_loc, o_peer, lse_peer)
@@ -373,8 +376,8 @@ class DecodeRingSim:
     * owner (ring_backend.py:652-689): ``assignee = growth_assignee(pos)``;
       ``ship`` = the previous step's pending token; local partial over
       ``own chunk + owned growth + current token`` (causal at ``len-1``: every
-      key visible); the current token joins the owned growth or becomes the
-      pending token;
+      key visible, or the last ``window`` of them with a sliding window); the
+      current token joins the owned growth or becomes the pending token;
     * the packet visits peers 1..N-1 in order (ring_decode.py:187-259): a node
       appends shipped growth when it is the target, then merges its partial
       over ``snapshot + its growth`` into the accumulator.
@@ -383,7 +386,9 @@ class DecodeRingSim:
     every ring member (``growth_of[i]`` for transport index i).
     """
 
-    def __init__(self, peer_chunks, own_chunk, scale: float, policy: str = "rr"):
+    def __init__(self, peer_chunks, own_chunk, scale: float, policy: str = "rr",
+                 window: int | None = None):
+        self.window = window
         self.peer_chunks = [(k.float(), v.float()) for k, v in peer_chunks]
         self.own_k, self.own_v = own_chunk[0].float(), own_chunk[1].float()
         self.scale = scale
@@ -410,7 +415,7 @@ class DecodeRingSim:
         owner_t = 0
         k_loc, v_loc = self._cat(self.own_k, self.own_v,
                                  self.growth_of[owner_t] + [(k_cur, v_cur)])
-        o, lse = attn_with_lse(q, k_loc, v_loc, self.scale, k_loc.shape[0] - 1)
+        o, lse = attn_with_lse(q, k_loc, v_loc, self.scale, k_loc.shape[0] - 1, self.window)
         if a == self.n - 1:
             self.growth_of[owner_t].append((k_cur, v_cur))
         else:

@@ -181,13 +181,13 @@ def test_decode_workspace_bytes(L):
 
 def _fwd(L, **kw):
     a = dict(q=16, k=16, v=16, out=16, lse=16, tq=4, tk=4, h=28, hkv=4, d=128,
-             st=8, causal=1, off=0, dtype=_lib.DTYPE_BF16, scale=0.088)
+             st=8, causal=1, off=0, window=0, dtype=_lib.DTYPE_BF16, scale=0.088)
     a.update(kw)
     s = a["st"]
     return L.hcp_attn_fwd_lse(a["q"], a["k"], a["v"], a["out"], a["lse"], a["tq"], a["tk"],
                               a["h"], a["hkv"], a["d"], s * a["h"], s, s * a["hkv"], s,
                               s * a["hkv"], s, s * a["h"], s, a["tq"], a["scale"],
-                              a["causal"], a["off"], a["dtype"], None)
+                              a["causal"], a["off"], a["window"], a["dtype"], None)
 
 
 def test_argument_validation_status_codes(L):
@@ -201,6 +201,8 @@ def test_argument_validation_status_codes(L):
     assert _fwd(L, q=24) == _lib.HCP_EINVAL          # not 16-byte aligned
     assert _fwd(L, st=12) == _lib.HCP_EINVAL         # stride not a multiple of 8
     assert _fwd(L, tq=0) == _lib.HCP_OK              # nothing to do, nothing launched
+    assert _fwd(L, window=-1) == _lib.HCP_EINVAL
+    assert b"negative window" in L.hcp_last_error()
     rc = L.hcp_merge_attn_states(16, 8, 8, 7, None, 0, 16, 8, 8, 1, 16, 4, 16, 8, 8, 1, 16, 4,
                                  4, 1, 8, None)
     assert rc == _lib.HCP_EUNSUPPORTED  # out dtype 7

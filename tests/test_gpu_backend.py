@@ -61,7 +61,7 @@ def _clean(monkeypatch):
 
 
 def _run(dev, layout, reqs, dtype=torch.bfloat16, seed=61, split=0, staged_chunks=None,
-         monkeypatch=None):
+         monkeypatch=None, window=None):
     """reqs: list of (tq, tk).  staged_chunks: per request list of chunk lengths
     (peer prefix = their concatenation) or None."""
     gen = torch.Generator().manual_seed(seed)
@@ -74,7 +74,7 @@ def _run(dev, layout, reqs, dtype=torch.bfloat16, seed=61, split=0, staged_chunk
     bt = _block_table(gen, seq_lens, nb)
     query = randn(gen, (qsl[-1] + 5, H, D), dtype)  # 5 padding rows past num_actual
     peers = None
-    impl = rb.HcpRingAttentionImpl(H, D, scale_for(D), HKV)
+    impl = rb.HcpRingAttentionImpl(H, D, scale_for(D), HKV, sliding_window=window)
     layer = types.SimpleNamespace(layer_name="model.layers.3.self_attn.attn")
     if split:
         monkeypatch.setenv("HCP_RING_SPLIT_TOKENS", str(split))
@@ -102,7 +102,7 @@ def _run(dev, layout, reqs, dtype=torch.bfloat16, seed=61, split=0, staged_chunk
     assert ret is output
     ref = orc.ring_forward(query.float(), cache.float(), layout, qsl, seq_lens, bt,
                            scale_for(D), peers=peers, split_tokens=split,
-                           out_dtype=torch.float32)
+                           out_dtype=torch.float32, window=window)
     n = qsl[-1]
     assert max_err(output[:n], ref[:n]) <= OUT_TOL[dtype]
     assert torch.all(output[n:] == 7.0)  # rows past num_actual_tokens untouched
@@ -140,6 +140,25 @@ def test_forward_decode_batch_uses_splitkv(dev):
     reqs = [(1, 513), (1, 2048 + 700), (1, 1), (1, 64 + 33)]
     staged = [[512], [2048], None, [64]]
     _run(dev, "v031", reqs, staged_chunks=staged)
+    assert rb.IMPL_STATS["decode_hip"] == 1
+
+
+@pytest.mark.parametrize("window", [1, 37, 256, 5000])
+def test_forward_sliding_window(dev, window, monkeypatch):
+    """sliding_window reaches every causal pass (no peer, the split env's n_a
+    rows and local rest) and never the peer pass (ring_backend.py:786-830)."""
+    _run(dev, "v031", [(300, 300), (17, 517), (1, 40), (129, 1000)], window=window)
+    _run(dev, "v023", [(300, 900), (200, 256), (64, 1100), (5, 700)], split=700,
+         monkeypatch=monkeypatch, window=window)
+
+
+@pytest.mark.parametrize("window", [1, 100, 3000])
+def test_forward_sliding_window_staged_and_decode(dev, window):
+    _run(dev, "v031", [(256, 256 + 512), (100, 100 + 64 + 128), (40, 40 + 2048)],
+         staged_chunks=[[512], [64, 128], [1024, 1024]], window=window)
+    # decode batch: the local segment is cut to its last `window` keys
+    _run(dev, "v031", [(1, 513), (1, 2048 + 700), (1, 1), (1, 64 + 33)],
+         staged_chunks=[[512], [2048], None, [64]], window=window)
     assert rb.IMPL_STATS["decode_hip"] == 1
 
 

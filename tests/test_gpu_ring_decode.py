@@ -175,7 +175,8 @@ def _slot(bt_row, pos):
 class _Req:
     """One decode-ring request: its prefix peers, pool blocks and oracle."""
 
-    def __init__(self, gen, dtype, dev, cache_cpu, layout, blocks, peer_lens, own_len, policy):
+    def __init__(self, gen, dtype, dev, cache_cpu, layout, blocks, peer_lens, own_len, policy,
+                 window=None):
         self.peer_k = [randn(gen, (n, HKV, D), dtype) for n in peer_lens]
         self.peer_v = [randn(gen, (n, HKV, D), dtype) for n in peer_lens]
         self.plen = sum(peer_lens)
@@ -183,7 +184,8 @@ class _Req:
         self.prompt = self.plen + own_len
         self.bt_row = blocks
         own = orc.gather_paged(cache_cpu.float(), blocks, self.plen, own_len, layout)
-        self.sim = orc.DecodeRingSim(list(zip(self.peer_k, self.peer_v)), own, scale_for(D), policy)
+        self.sim = orc.DecodeRingSim(list(zip(self.peer_k, self.peer_v)), own, scale_for(D), policy,
+                                     window)
         self.steps = 0
 
 
@@ -197,7 +199,7 @@ def _meta(dev, qsl, seq_lens, bt):
 
 
 def _setup(dev, dtype, layout, n_req, peer_lens, own_len, policy, seed, monkeypatch,
-           extra_blocks=0):
+           extra_blocks=0, window=None):
     gen = torch.Generator().manual_seed(seed)
     if policy != "rr":
         monkeypatch.setenv("HCP_RING_DECODE_GROWTH", policy)
@@ -210,7 +212,8 @@ def _setup(dev, dtype, layout, n_req, peer_lens, own_len, policy, seed, monkeypa
     reqs = []
     for r in range(n_req):
         blocks = perm[r * per:(r + 1) * per].clone()
-        reqs.append(_Req(gen, dtype, dev, cache_cpu, layout, blocks, peer_lens, own_len, policy))
+        reqs.append(_Req(gen, dtype, dev, cache_cpu, layout, blocks, peer_lens, own_len, policy,
+                         window))
     # a ring of nodes per request (each node's first chunk key is the one
     # it serves, ring_decode.py:226-228)
     n_peer = len(peer_lens)
@@ -367,3 +370,20 @@ def test_backend_decode_ring_next_to_prefill(dev, monkeypatch):
         assert max_err(out[:ptq], ref[:ptq]) <= OUT_TOL[dtype]
         k_written, _ = orc.gather_paged(c, pbt, ptk - ptq, ptq, "v031")
         assert torch.equal(k_written, key[:ptq])
+
+
+@pytest.mark.parametrize("window", [1, 7, 40])
+def test_backend_decode_ring_sliding_window(dev, window, monkeypatch):
+    """The owner's local partial is causal at len - 1 over own chunk + owned
+    growth + current token (ring_backend.py:672-679): with a sliding window
+    it keeps the last `window` keys of that concatenation; the nodes' partials
+    are non-causal and unwindowed."""
+    dtype = torch.float16
+    gen, cache_cpu, cache, reqs, transports = _setup(dev, dtype, "v031", 1, [40, 33], 29, "rr",
+                                                     31, monkeypatch, window=window)
+    impl = rb.HcpRingAttentionImpl(H, D, scale_for(D), HKV, sliding_window=window)
+    layer = types.SimpleNamespace(layer_name=LAYER)
+    for t in range(7):
+        _, refs, *_ = _decode_step(dev, dtype, impl, layer, gen, cache, reqs, monkeypatch)
+        for got, want in refs:
+            assert max_err(got, want) <= OUT_TOL[dtype], t

@@ -17,7 +17,7 @@ import torch
 from oracle import ring_oracle as orc
 
 
-def brute(q, k, v, scale, off):
+def brute(q, k, v, scale, off, window=None):
     """float64 loops: out[i,h] = sum_j w_j v_j, lse = log sum_j exp(s_j)."""
     q = q.double().numpy()
     k = k.double().numpy()
@@ -30,7 +30,8 @@ def brute(q, k, v, scale, off):
     for i in range(tq):
         for hh in range(h):
             kh = hh // g
-            vis = [j for j in range(tk) if off is None or j <= off + i]
+            vis = [j for j in range(tk) if off is None or
+                   (j <= off + i and (window is None or j > off + i - window))]
             if not vis:
                 continue
             s = np.array([scale * float(np.dot(q[i, hh], k[j, kh])) for j in vis])
@@ -409,3 +410,67 @@ def test_decode_ring_sim_catches_a_lost_shipment():
         bo, _ = _brute_t(q, torch.cat(allk), torch.cat(allv), scale, None)
         worst = max(worst, (o.double() - bo).abs().max().item())
     assert worst > 1e-3
+
+
+
+# ---------------------------------------------------------------------------
+# Sliding window (ring_backend.py:372,397-398)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("tq,tk,off,w", [(5, 9, 4, 1), (7, 12, 5, 3), (6, 6, 0, 2),
+                                         (4, 10, 8, 20), (5, 8, -2, 3), (3, 4, 9, 2)])
+def test_window_vs_float64_brute(tq, tk, off, w):
+    g = torch.Generator().manual_seed(tq * 31 + w)
+    q, k, v = rnd(g, tq, 4, 8), rnd(g, tk, 2, 8), rnd(g, tk, 2, 8)
+    o, lse = orc.attn_with_lse(q, k, v, 0.3, off, w)
+    bo, bl = brute(q, k, v, 0.3, off, w)
+    assert np.abs(o.double().numpy() - bo).max() < 1e-5
+    finite = np.isfinite(bl)
+    assert np.array_equal(finite, np.isfinite(lse.double().numpy()))
+    if finite.any():
+        assert np.abs(lse.double().numpy()[finite] - bl[finite]).max() < 1e-5
+
+
+def test_window_closed_forms():
+    """w = 1: every row sees only its own position -- out = v there and
+    lse = scale q.k there.  A window wider than the causal range is no
+    window at all."""
+    g = torch.Generator().manual_seed(12)
+    q, k, v = rnd(g, 6, 4, 8), rnd(g, 10, 2, 8), rnd(g, 10, 2, 8)
+    o, lse = orc.attn_with_lse(q, k, v, 0.5, 4, 1)
+    for i in range(6):
+        j = 4 + i
+        for h in range(4):
+            assert torch.allclose(o[i, h], v[j, h // 2], atol=1e-6)
+            assert abs(lse[h, i].item() - 0.5 * float(q[i, h] @ k[j, h // 2])) < 1e-5
+    o1, l1 = orc.attn_with_lse(q, k, v, 0.5, 4, 10)
+    o2, l2 = orc.attn_with_lse(q, k, v, 0.5, 4, None)
+    assert torch.allclose(o1, o2) and torch.allclose(l1, l2)
+
+
+def test_decode_ring_sim_window_one_sees_the_current_token_locally():
+    """With window 1 the owner's local partial is the current token alone,
+    so the ring's result is attention over every peer key (snapshots and
+    their growth) plus the current token -- not the owner's chunk or its
+    growth."""
+    g = torch.Generator().manual_seed(77)
+    H, HKV, D, scale = 4, 2, 16, 0.25
+    peers = [(rnd(g, 5, HKV, D), rnd(g, 5, HKV, D)), (rnd(g, 3, HKV, D), rnd(g, 3, HKV, D))]
+    own = (rnd(g, 4, HKV, D), rnd(g, 4, HKV, D))
+    sim = orc.DecodeRingSim(peers, own, scale, "rr", window=1)
+    peer_keys = [[peers[0]], [peers[1]]]
+    pending = None
+    for t in range(7):
+        pos = 12 + t
+        q = rnd(g, 1, H, D)
+        kc, vc = rnd(g, 1, HKV, D), rnd(g, 1, HKV, D)
+        if pending is not None:
+            peer_keys[pending[0]].append(pending[1])
+            pending = None
+        o, lse = sim.step(q, kc, vc, pos)
+        ks = [kv[0] for row in peer_keys for kv in row] + [kc]
+        vs = [kv[1] for row in peer_keys for kv in row] + [vc]
+        bo, bl = _brute_t(q, torch.cat(ks), torch.cat(vs), scale, None)
+        assert (o.double() - bo).abs().max() < 1e-5, t
+        assert (lse.double() - bl).abs().max() < 1e-5, t
+        if pos % 3 != 2:  # growth index of a peer: shipped next step
+            pending = (pos % 3, (kc, vc))
