@@ -34,10 +34,11 @@
 //  * K and V tiles (64 keys x D, row-major, 16-byte slots XOR-swizzled by
 //    2*(row&3) | (row>>2 & 1) so both the K reads and the transposing V reads
 //    are bank-conflict free) go HBM/L2 -> LDS with buffer_load ... lds (no
-//    register staging, no VALU work), one load instruction every four MFMAs
-//    of the phase that does not read that buffer.  Two K and two V buffers:
-//    iteration n reads K(n+1), V(n) and fills K(n+2), V(n+1); one barrier per
-//    tile.
+//    register staging, no VALU work), one load instruction every two MFMAs of
+//    phase A, K and V alternating.  Two K and two V buffers: iteration n reads
+//    K(n+1), V(n) and fills K(n+2), V(n+1) (both buffers free since the last
+//    barrier, so all its loads start in phase A and have phase B to land);
+//    one barrier per tile.
 //  * Lazy rescale: the running max used as the exponent reference is only
 //    raised when some row's tile max exceeds it by more than 2^8; otherwise P
 //    values are bounded by 256 and the O rescale (64 multiplies per lane) is
@@ -55,9 +56,6 @@
 
 namespace hcp {
 
-#ifndef HCP_MFMA_PRIO
-#define HCP_MFMA_PRIO 3
-#endif
 #ifndef HCP_KPF
 #define HCP_KPF 3  // K fragment reads issued this many MFMAs ahead (phase A)
 #endif
@@ -74,6 +72,7 @@ constexpr float kRescaleThresh = 8.0f;  // log2 units: P <= 2^8 between rescales
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+
 #define HCP_LDS(T) __attribute__((address_space(3))) T
 
 // XOR swizzle of the 16-byte slot index of tile row `row`.  gfx950 LDS has 64
@@ -314,7 +313,7 @@ fa_fwd_kernel(FwdParams p) {
         rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
         static_cast<int>(goff[i]), 0, 0, 0);
   };
-  // load i of a tile is issued under MFMA step LOAD_STEP(i) of a phase
+  // phase A issues one K or V load instruction every kLoadEvery/2 MFMAs
   constexpr int kLoadEvery = 4;
 
   // ---- LDS read addresses (loop invariant, per lane) ----
@@ -489,12 +488,41 @@ fa_fwd_kernel(FwdParams p) {
   // Phase A: S_nxt = K(n+1) Q^T (2*KSTEPS MFMAs, K fragments read from LDS
   // three MFMAs ahead) while P(n) = exp2(c S_cur - m_ref) and its P^T
   // fragments are formed, EA scores per MFMA.
+  // V^T fragment j (16 keys x 32 head-dim columns) of tile Vs, transposing reads
+  constexpr int VR = HCP_VPF + 1;  // V fragment ring
+  auto vread_at = [&](const HCP_LDS(char)* Vs, int j) __attribute__((always_inline)) {
+    const int t = j / DBLK, db = j % DBLK;
+    const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
+    const i16x4 hi = lds_read_tr(Vs + voff[db][1] + (16 * t) * ROWB);
+    u32x4 w;
+    w[0] = __builtin_bit_cast(u32x2, lo)[0];
+    w[1] = __builtin_bit_cast(u32x2, lo)[1];
+    w[2] = __builtin_bit_cast(u32x2, hi)[0];
+    w[3] = __builtin_bit_cast(u32x2, hi)[1];
+    return w;
+  };
+
+  // P for score pair `pair` (scores 2*pair, 2*pair+1 of the lane's 32):
+  // exp2(c S - m) in place and packed into its P^T fragment
+  auto exp_pair = [&](int pair, f32x16 (&Sc)[2], float m_use) __attribute__((always_inline)) {
+    const int x = 2 * pair;  // 0..31, even
+    const int h = x >> 4, r = x & 15;
+    const float p0 = fast_exp2(__builtin_fmaf(Sc[h][r], c, -m_use));
+    const float p1 = fast_exp2(__builtin_fmaf(Sc[h][r + 1], c, -m_use));
+    Sc[h][r] = p0;
+    Sc[h][r + 1] = p1;
+    // P^T fragment 2h + (r >> 3) holds regs 8t .. 8t+7 of half h
+    u32x4 w = __builtin_bit_cast(u32x4, pf[2 * h + (r >> 3)]);
+    w[(r & 7) >> 1] = pack2<T>(p0, p1);
+    pf[2 * h + (r >> 3)] = as_vec8<V8>(w);
+  };
   constexpr int NA = 2 * KSTEPS;  // MFMAs in phase A
   constexpr int EA = 32 / NA;     // scores exponentiated per phase-A MFMA
   constexpr int NB = 4 * DBLK;    // MFMAs in phase B
   constexpr int EB = 32 / NB;     // scores summed / maxed per phase-B MFMA
   auto phase_a = [&](const HCP_LDS(char)* Ks, f32x16 (&Sc)[2], f32x16 (&Sn)[2],
-                     __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads)
+                     __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads,
+                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2)
       __attribute__((always_inline)) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     constexpr int KR = HCP_KPF + 1;  // K fragment ring
@@ -510,22 +538,20 @@ fa_fwd_kernel(FwdParams p) {
         kf[j % KR] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
       }
       Sn[blk] = E::mfma32(kf[st % KR], qf[s], s == 0 ? f32x16{} : Sn[blk]);
-      if (loads && st % kLoadEvery == kLoadEvery / 2 && st / kLoadEvery < NI)
-        load_one(rs, st / kLoadEvery, ldst);
-      // scores st*EA .. st*EA+EA-1 of the current tile: half h, regs r..
-#pragma unroll
-      for (int q = 0; q < EA; q += 2) {
-        const int x = st * EA + q;  // 0..31, even
-        const int h = x >> 4, r = x & 15;
-        const float p0 = fast_exp2(__builtin_fmaf(Sc[h][r], c, -m_use));
-        const float p1 = fast_exp2(__builtin_fmaf(Sc[h][r + 1], c, -m_use));
-        Sc[h][r] = p0;
-        Sc[h][r + 1] = p1;
-        // P^T fragment 2h + (r >> 3) holds regs 8t .. 8t+7 of half h
-        u32x4 w = __builtin_bit_cast(u32x4, pf[2 * h + (r >> 3)]);
-        w[(r & 7) >> 1] = pack2<T>(p0, p1);
-        pf[2 * h + (r >> 3)] = as_vec8<V8>(w);
+      // K(n+2) and V(n+1) tile loads, alternating, one every kLoadEvery/2
+      // MFMAs: V's buffer was freed by the previous barrier, and a whole
+      // phase B passes before this iteration's barrier waits for the loads
+      constexpr int LE = kLoadEvery / 2;
+      if (loads && st % LE == 0 && st / LE < 2 * NI) {
+        const int i = st / LE;
+        if (i % 2 == 0)
+          load_one(rs, i / 2, ldst);
+        else
+          load_one(rs2, i / 2, ldst2);
       }
+      // scores st*EA .. st*EA+EA-1 of the current tile
+#pragma unroll
+      for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, m_use);
       __builtin_amdgcn_sched_barrier(0);
     }
     // P(n) is complete here: keep its computation in this phase (all its uses
@@ -539,21 +565,9 @@ fa_fwd_kernel(FwdParams p) {
   // Phase B: O += V(n)^T P(n)^T (NB MFMAs, transposing V reads two MFMAs
   // ahead) while l gathers P(n)'s row sum and mh the raw max of S_nxt.
   auto phase_b = [&](const HCP_LDS(char)* Vs, const f32x16 (&Sc)[2], const f32x16 (&Sn)[2],
-                     float& mh, __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads)
-      __attribute__((always_inline)) {
-    constexpr int VR = HCP_VPF + 1;  // V fragment ring
+                     float& mh) __attribute__((always_inline)) {
     u32x4 vf[VR];
-    auto vread = [&](int j) __attribute__((always_inline)) {
-      const int t = j / DBLK, db = j % DBLK;
-      const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
-      const i16x4 hi = lds_read_tr(Vs + voff[db][1] + (16 * t) * ROWB);
-      u32x4 w;
-      w[0] = __builtin_bit_cast(u32x2, lo)[0];
-      w[1] = __builtin_bit_cast(u32x2, lo)[1];
-      w[2] = __builtin_bit_cast(u32x2, hi)[0];
-      w[3] = __builtin_bit_cast(u32x2, hi)[1];
-      return w;
-    };
+    auto vread = [&](int j) __attribute__((always_inline)) { return vread_at(Vs, j); };
 #pragma unroll
     for (int j = 0; j < HCP_VPF; ++j) vf[j] = vread(j);
     float rs0 = Sc[0][0], rs1 = Sc[0][1];
@@ -563,8 +577,6 @@ fa_fwd_kernel(FwdParams p) {
       const int t = st / DBLK, db = st % DBLK;
       if (st + HCP_VPF < NB) vf[(st + HCP_VPF) % VR] = vread(st + HCP_VPF);
       oacc[db] = E::mfma32(as_vec8<V8>(vf[st % VR]), pf[t], oacc[db]);
-      if (loads && st % kLoadEvery == kLoadEvery / 2 && st / kLoadEvery < NI)
-        load_one(rs, st / kLoadEvery, ldst);
 #pragma unroll
       for (int q = 0; q < EB; q += 2) {
         const int x = st * EB + q;
@@ -595,8 +607,8 @@ fa_fwd_kernel(FwdParams p) {
                      HCP_LDS(char)* vload, const HCP_LDS(char)* Ks,
                      const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
     // loads for the next iteration: K(n+2) -> kload, V(n+1) -> vload.
-    // Contiguous segments issue them one at a time under the MFMAs of phases
-    // A (K) and B (V); paged segments (block-table lookups) issue them here.
+    // Contiguous segments issue them one at a time under the MFMAs of phase
+    // A; paged segments (block-table lookups) issue them here.
     bool spread = false;
     const __amdgpu_buffer_rsrc_t rsk = tile_rsrc(kseg, n + 2);  // unused when paged
     const __amdgpu_buffer_rsrc_t rsv = tile_rsrc(vseg, n + 1);
@@ -619,10 +631,10 @@ fa_fwd_kernel(FwdParams p) {
       }
     }
     if (n < wtiles) {
-      phase_a(Ks, Sc, Sn, rsk, kload, spread);
+      phase_a(Ks, Sc, Sn, rsk, kload, spread, rsv, vload);
       if (needs_mask(n + 1)) apply_mask(Sn, n + 1);
       float mh;
-      phase_b(Vs, Sc, Sn, mh, rsv, vload, spread);
+      phase_b(Vs, Sc, Sn, mh);
       if (n + 1 < wtiles) check_rescale(mh);
     }
     __syncthreads();  // waits for this iteration's tile loads (vmcnt(0)) first
