@@ -104,7 +104,7 @@ __device__ __forceinline__ i16x4 lds_read_tr(const HCP_LDS(char)* p) {
 }
 
 template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
+__global__ __attribute__((amdgpu_flat_work_group_size(kFwdThreads, kFwdThreads),
                           amdgpu_waves_per_eu(HCP_FWD_WAVES_PER_EU, HCP_FWD_WAVES_PER_EU))) void
 fa_fwd_kernel(FwdParams p) {
   using E = Elem<T>;

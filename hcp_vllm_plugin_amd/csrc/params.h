@@ -6,9 +6,12 @@
 
 namespace hcp {
 
-constexpr int kFwdBM = 128;  // query rows per prefill workgroup
-constexpr int kFwdBN = 64;   // keys per prefill tile
-constexpr int kFwdThreads = 256;
+#ifndef HCP_FWD_WAVES
+#define HCP_FWD_WAVES 4  // waves per prefill workgroup, 32 query rows each
+#endif
+constexpr int kFwdThreads = 64 * HCP_FWD_WAVES;
+constexpr int kFwdBM = 32 * HCP_FWD_WAVES;  // query rows per prefill workgroup
+constexpr int kFwdBN = 64;                  // keys per prefill tile
 
 struct FwdParams {
   const void* q;
