@@ -56,7 +56,7 @@ EXPORTED_SYMBOLS = (
     "hcp_reshape_and_cache",
 )
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class KvSegment(ctypes.Structure):
@@ -72,7 +72,7 @@ class KvSegment(ctypes.Structure):
         ("start", ctypes.c_int64),
         ("len", ctypes.c_int64),
         ("block_size", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
     ]
 
 

@@ -232,17 +232,52 @@ fa_fwd_kernel(FwdParams p) {
     vseg = reinterpret_cast<const char*>(e.kv.v_addr) + base;
   }
 
+  // Paged segments whose cache spans less than 4 GiB from this head's base
+  // are read with buffer loads over one descriptor for the whole cache: the
+  // per-lane 32-bit byte offset of a row replaces its block id, loads are
+  // spread under phase A like contiguous ones, and a block id past the cache
+  // reads zeros instead of faulting.  Larger caches use global loads.
+  bool pbuf = false;
+  __amdgpu_buffer_rsrc_t rs_pk, rs_pv;
+  if constexpr (PAGED) {
+    const uint64_t span = static_cast<uint64_t>(e.kv.num_blocks) * static_cast<uint64_t>(blockb);
+    pbuf = e.kv.num_blocks > 0 && span < (uint64_t{1} << 32) && e.kv.block_size <= BN;
+    const int nrec = pbuf ? static_cast<int>(static_cast<uint32_t>(span)) : 0;
+    rs_pk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kseg), 0, nrec, kBufferRsrcWord3);
+    rs_pv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vseg), 0, nrec, kBufferRsrcWord3);
+  }
+
   // paged: block ids of the lane's rows.  Tile j's K is issued at iteration
   // j-2 and its V at iteration j-1, so three tiles' ids are live: bid_v (tile
   // n+1), bid_k (tile n+2) and bid_f (tile n+3, fetched during iteration n).
-  int bid_v[NI], bid_k[NI], bid_f[NI];
-  auto fetch_blocks = [&](int tile_idx, int (&dst)[NI]) __attribute__((always_inline)) {
+  // With buffer loads, a tile's ids become byte offsets from the head's base
+  // at the start of the iteration that issues its K -- one iteration after
+  // the fetch, so the conversion never waits on the block-table load.
+  uint32_t bid_v[NI], bid_k[NI], bid_f[NI];
+  auto fetch_blocks = [&](int tile_idx, uint32_t (&dst)[NI]) __attribute__((always_inline)) {
     if constexpr (PAGED) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         int key = tile_idx * BN + lrow(i);
         key = key < kv_len ? key : kv_len - 1;
-        dst[i] = bt[(e.kv.start + key) >> bs_shift];
+        dst[i] = static_cast<uint32_t>(bt[(e.kv.start + key) >> bs_shift]);
+      }
+    }
+  };
+  auto to_offsets = [&](int tile_idx, uint32_t (&ids)[NI]) __attribute__((always_inline)) {
+    if constexpr (PAGED) {
+      // block_size <= BN: a row's offset inside its block does not depend on
+      // the tile, except on a ragged tile whose rows past the end are clamped
+      // to the last key (a valid row: unused cache slots may hold NaNs)
+      const bool ragged = tile_idx * BN + BN > kv_len;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        int key = tile_idx * BN + lrow(i);
+        if (ragged) key = key < kv_len ? key : kv_len - 1;
+        const uint32_t x = static_cast<uint32_t>(e.kv.start + key);
+        ids[i] = ids[i] * static_cast<uint32_t>(blockb) +
+                 (x & static_cast<uint32_t>(bs_mask)) * static_cast<uint32_t>(rowb_g) +
+                 lchunk(i) * 16u;
       }
     }
   };
@@ -257,11 +292,20 @@ fa_fwd_kernel(FwdParams p) {
   // Issue the global->LDS loads of one tile of K or V.  Ragged tiles clamp
   // their key rows into the segment (those rows are masked in S, and their
   // finite V values meet P = 0), so no load leaves the segment.
-  auto issue = [&](const char* seg, int tile_idx, const int (&bids)[NI], HCP_LDS(char)* dst)
-      __attribute__((always_inline)) {
+  auto issue = [&](const char* seg, int tile_idx, const uint32_t (&bids)[NI],
+                   HCP_LDS(char)* dst) __attribute__((always_inline)) {
     const int n0 = tile_idx * BN;
     const bool ragged = n0 + BN > kv_len;
     if constexpr (PAGED) {
+      if (pbuf) {
+        const __amdgpu_buffer_rsrc_t rs = seg == kseg ? rs_pk : rs_pv;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
+              static_cast<int>(bids[i]), 0, 0, 0);
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         int key = n0 + lrow(i);
@@ -312,6 +356,13 @@ fa_fwd_kernel(FwdParams p) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
         static_cast<int>(goff[i]), 0, 0, 0);
+  };
+  // the same with the lane's offset given (paged rows)
+  auto load_at = [&](__amdgpu_buffer_rsrc_t rs, uint32_t o, int i, HCP_LDS(char)* dst)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
+        static_cast<int>(o), 0, 0, 0);
   };
   // phase A issues one K or V load instruction every kLoadEvery/2 MFMAs
   constexpr int kLoadEvery = 4;
@@ -522,7 +573,8 @@ fa_fwd_kernel(FwdParams p) {
   constexpr int EB = 32 / NB;     // scores summed / maxed per phase-B MFMA
   auto phase_a = [&](const HCP_LDS(char)* Ks, f32x16 (&Sc)[2], f32x16 (&Sn)[2],
                      __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads,
-                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2)
+                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2, bool loads2,
+                     const uint32_t (&ko)[NI], const uint32_t (&vo)[NI])
       __attribute__((always_inline)) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     constexpr int KR = HCP_KPF + 1;  // K fragment ring
@@ -542,12 +594,19 @@ fa_fwd_kernel(FwdParams p) {
       // MFMAs: V's buffer was freed by the previous barrier, and a whole
       // phase B passes before this iteration's barrier waits for the loads
       constexpr int LE = kLoadEvery / 2;
-      if (loads && st % LE == 0 && st / LE < 2 * NI) {
+      if (st % LE == 0 && st / LE < 2 * NI) {
         const int i = st / LE;
-        if (i % 2 == 0)
-          load_one(rs, i / 2, ldst);
-        else
-          load_one(rs2, i / 2, ldst2);
+        if (i % 2 == 0) {
+          if (loads) {
+            if constexpr (PAGED) load_at(rs, ko[i / 2], i / 2, ldst);
+            else load_one(rs, i / 2, ldst);
+          }
+        } else {
+          if (loads2) {
+            if constexpr (PAGED) load_at(rs2, vo[i / 2], i / 2, ldst2);
+            else load_one(rs2, i / 2, ldst2);
+          }
+        }
       }
       // scores st*EA .. st*EA+EA-1 of the current tile
 #pragma unroll
@@ -607,20 +666,30 @@ fa_fwd_kernel(FwdParams p) {
                      HCP_LDS(char)* vload, const HCP_LDS(char)* Ks,
                      const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
     // loads for the next iteration: K(n+2) -> kload, V(n+1) -> vload.
-    // Contiguous segments issue them one at a time under the MFMAs of phase
-    // A; paged segments (block-table lookups) issue them here.
-    bool spread = false;
-    const __amdgpu_buffer_rsrc_t rsk = tile_rsrc(kseg, n + 2);  // unused when paged
-    const __amdgpu_buffer_rsrc_t rsv = tile_rsrc(vseg, n + 1);
+    // Contiguous and buffer-paged tiles are issued one load at a time under
+    // the MFMAs of phase A; globally-paged tiles are issued here.
+    bool spread;
+    __amdgpu_buffer_rsrc_t rsk, rsv;
+    bool lk = true, lv = true;  // K(n+2) / V(n+1) exist (paged) or are clamped (contiguous)
     if constexpr (PAGED) {
-      if (n + 2 < ntiles) issue(kseg, n + 2, bid_k, kload);
-      if (n + 1 < ntiles) issue(vseg, n + 1, bid_v, vload);
-#pragma unroll
-      for (int i = 0; i < NI; ++i) bid_v[i] = bid_k[i];
+      rsk = rs_pk;
+      rsv = rs_pv;
+      lk = n + 2 < ntiles;
+      lv = n + 1 < ntiles;
+      if (pbuf && lk) to_offsets(n + 2, bid_k);  // fetched one iteration ago
+      if (!pbuf) {
+        if (lk) issue(kseg, n + 2, bid_k, kload);
+        if (lv) issue(vseg, n + 1, bid_v, vload);
+      }
       if (n + 3 < ntiles) fetch_blocks(n + 3, bid_f);
-#pragma unroll
-      for (int i = 0; i < NI; ++i) bid_k[i] = bid_f[i];
+      spread = pbuf && n < wtiles;
+      if (pbuf && !spread) {
+        if (lk) issue(kseg, n + 2, bid_k, kload);
+        if (lv) issue(vseg, n + 1, bid_v, vload);
+      }
     } else {
+      rsk = tile_rsrc(kseg, n + 2);
+      rsv = tile_rsrc(vseg, n + 1);
       spread = n < wtiles;
       if (!spread) {
 #pragma unroll
@@ -631,11 +700,21 @@ fa_fwd_kernel(FwdParams p) {
       }
     }
     if (n < wtiles) {
-      phase_a(Ks, Sc, Sn, rsk, kload, spread, rsv, vload);
+      if constexpr (PAGED)
+        phase_a(Ks, Sc, Sn, rsk, kload, spread && lk, rsv, vload, spread && lv, bid_k, bid_v);
+      else
+        phase_a(Ks, Sc, Sn, rsk, kload, spread, rsv, vload, spread, goff, goff);
       if (needs_mask(n + 1)) apply_mask(Sn, n + 1);
       float mh;
       phase_b(Vs, Sc, Sn, mh);
       if (n + 1 < wtiles) check_rescale(mh);
+    }
+    if constexpr (PAGED) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        bid_v[i] = bid_k[i];
+        bid_k[i] = bid_f[i];
+      }
     }
     __syncthreads();  // waits for this iteration's tile loads (vmcnt(0)) first
   };
@@ -648,10 +727,12 @@ fa_fwd_kernel(FwdParams p) {
   // ---- prologue: K(0), K(1), V(0) in flight; S(0) = K(0) Q^T ----
   if (ntiles > 0) {
     fetch_blocks(0, bid_f);
+    if (pbuf) to_offsets(0, bid_f);
     issue(kseg, 0, bid_f, K0);
     issue(vseg, 0, bid_f, V0);
     if (ntiles > 1) {
       fetch_blocks(1, bid_v);
+      if (pbuf) to_offsets(1, bid_v);
       issue(kseg, 1, bid_v, K1);
     }
     if (ntiles > 2) fetch_blocks(2, bid_k);

@@ -58,6 +58,10 @@ class PagedCache:
     stride_head: int
     stride_block: int
 
+    @property
+    def num_blocks(self) -> int:
+        return int(self.cache.shape[0])
+
     @classmethod
     def from_tensor(cls, cache: torch.Tensor) -> "PagedCache":
         if cache.stride(-1) != 1:
@@ -141,6 +145,7 @@ def segment_paged(pc: PagedCache, block_table_row: torch.Tensor, start: int,
     s.start = start
     s.len = length
     s.block_size = pc.block_size
+    s.num_blocks = pc.num_blocks if pc.num_blocks < (1 << 31) else 0
     s._keep = (pc.cache, block_table_row)  # raw addresses inside: keep them alive
     return s
 

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 5
+#define HCP_ABI_VERSION 6
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -63,7 +63,10 @@ typedef enum hcp_dtype {
  * stride_head = bs*2D, stride_tok = 2D; file_connector.py:13-16,175-179)
  * and the vLLM 0.23 layout [nb, 2, bs, Hkv, D] (v_addr = cache + bs*Hkv*D,
  * stride_block = 2*bs*Hkv*D, stride_head = D, stride_tok = Hkv*D;
- * ring_backend.py:601,617-624).
+ * ring_backend.py:601,617-624).  With num_blocks given and the cache's
+ * num_blocks * stride_block bytes below 4 GiB the prefill kernel reads the
+ * paged segment with bounds-checked buffer loads (a block id past the cache
+ * reads zeros); otherwise with plain global loads.
  */
 typedef struct hcp_kv_segment {
   uint64_t k_addr;
@@ -75,7 +78,7 @@ typedef struct hcp_kv_segment {
   int64_t start;      /* first token of the segment inside its source */
   int64_t len;        /* number of keys in the segment (0 allowed) */
   int32_t block_size; /* power of two; ignored when contiguous */
-  int32_t reserved;
+  int32_t num_blocks; /* paged: blocks in the cache (ids must be below it), 0 = not given */
 } hcp_kv_segment;
 
 /*
