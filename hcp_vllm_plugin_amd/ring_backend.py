@@ -46,6 +46,7 @@ import enum
 import logging
 import os
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -58,6 +59,7 @@ from .varlen import (
     PagedCache,
     VarlenLaunch,
     make_entry,
+    paged_entry_array,
     segment_contiguous,
     segment_paged,
     trim_segment,
@@ -188,6 +190,33 @@ def _release_staged_for_request(first_block_id: int) -> None:
     else:
         for ck in PEER_REQ_MAP.pop(first_block_id, None) or []:
             drop_chunk_kv(ck)
+
+
+# Host copy of the step's attention metadata.  vLLM hands every layer the same
+# metadata object, so one device->host copy serves all layers of a step (the
+# reference syncs three times per layer, ring_backend.py:604-605).  Holding the
+# object keeps its identity from being reused by a later step's metadata.
+_STEP: dict = {"meta": None, "host": None, "bt": None, "fast": {}}
+
+
+def _host_metadata(attn_metadata):
+    """(query_start_loc, seq_lens, first block ids) as lists, and the block
+    table as contiguous int32, for this step's metadata."""
+    if _STEP["meta"] is attn_metadata:
+        return _STEP["host"], _STEP["bt"]
+    block_table = attn_metadata.block_table
+    if block_table.dtype != torch.int32:
+        block_table = block_table.to(torch.int32)
+    block_table = block_table.contiguous()
+    qsl_t = attn_metadata.query_start_loc
+    sl_t = attn_metadata.seq_lens
+    n = sl_t.shape[0]
+    fb = block_table[:, 0] if block_table.shape[1] > 0 else sl_t.new_zeros(n)
+    packed = torch.cat([qsl_t.reshape(-1).to(torch.int64), sl_t.reshape(-1).to(torch.int64),
+                        fb.reshape(-1).to(torch.int64)]).tolist()
+    host = (packed[:n + 1], packed[n + 1:2 * n + 1], packed[2 * n + 1:])
+    _STEP.update(meta=attn_metadata, host=host, bt=block_table, fast={})
+    return host, block_table
 
 
 def _forward_attn_metadata(layer):
@@ -531,20 +560,18 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         pc = PagedCache.from_tensor(kv_cache)
         if pc.num_kv_heads != self.num_kv_heads or pc.head_dim != self.head_size:
             raise ValueError("kv_cache shape does not match the layer's heads/head_size")
-        # small metadata tensors: one host sync, as the reference (:604-605)
-        qsl = attn_metadata.query_start_loc.tolist()
-        seq_lens = attn_metadata.seq_lens.tolist()
-        block_table = attn_metadata.block_table
-        if block_table.dtype != torch.int32:
-            block_table = block_table.to(torch.int32)
-        block_table = block_table.contiguous()
-        first_blocks = block_table[:, 0].tolist() if block_table.shape[1] > 0 else []
+        # small metadata tensors: one host sync per step (see _host_metadata)
+        (qsl, seq_lens, first_blocks), block_table = _host_metadata(attn_metadata)
         BATCH_STATS["max_reqs"] = max(BATCH_STATS["max_reqs"], len(seq_lens))
-        split = _split_tokens() if _ring_enabled() else 0
+        ring_on = _ring_enabled()
+        split = _split_tokens() if ring_on else 0
         layer_name = getattr(layer, "layer_name", "")
+        n = len(seq_lens)
+        if self._peer_free(ring_on, split, first_blocks, n):
+            self._forward_local_only(query, out, qsl, seq_lens, block_table, pc, kv_cache)
+            return output
 
         plan = self._plan(layer_name, qsl, seq_lens, block_table, first_blocks, pc, split)
-        n = len(seq_lens)
         is_decode = n > 0 and qsl == list(range(n + 1))
         ring_local = self._ring_local_segments(plan, pc, key, value, layer_name)
         if is_decode:
@@ -620,6 +647,65 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
                                    growth_v=gv, growth_target=target)
         IMPL_STATS["ring_decode_steps"] += 1
         return o
+
+    # -- batches with no peer KV and no decode-ring rows -------------------------
+    @staticmethod
+    def _peer_free(ring_on: bool, split: int, first_blocks, n: int) -> bool:
+        """No request of the batch takes a peer segment or the decode ring:
+        the plain causal pass over the paged cache (ring_backend.py:783-789)."""
+        if _decode_ring_enabled() and DECODE_RING_MAP and \
+                any(fb in DECODE_RING_MAP for fb in first_blocks):
+            return False
+        if not ring_on:
+            return True
+        if split > 0:
+            return False
+        if not PEER_KV_STAGING:
+            return True
+        return n > 1 and not any(fb in PEER_REQ_MAP for fb in first_blocks)
+
+    def _forward_local_only(self, query, out, qsl, seq_lens, block_table, pc, kv_cache):
+        """Causal attention of every request over its paged KV, the batch's
+        entries built with array operations (once per step and cache layout,
+        then only the layer's cache address changes): a split-KV decode for a
+        pure decode batch, else one varlen launch."""
+        n = len(seq_lens)
+        if n == 0:
+            return
+        is_decode = qsl == list(range(n + 1))
+        w = self.sliding_window
+        key = (is_decode, w, pc.layout, pc.stride_tok, pc.stride_head, pc.stride_block,
+               pc.block_size, pc.num_blocks, pc.v_addr - pc.k_addr)
+        tmpl = _STEP["fast"].get(key)
+        if tmpl is None:
+            qs = np.asarray(qsl[:-1], dtype=np.int64)
+            tq = np.diff(np.asarray(qsl, dtype=np.int64))
+            tk = np.asarray(seq_lens, dtype=np.int64)
+            rows = np.arange(n, dtype=np.int64)
+            if is_decode:
+                # one query at the end of its keys: all of them visible, or
+                # the last `w` of them (ring_backend.py:397-398)
+                start = np.zeros(n, np.int64) if w is None else np.maximum(tk - w, 0)
+                tmpl = paged_entry_array(pc, block_table, rows, rows, 1, 0, start, tk - start)
+            else:
+                sel = tq > 0
+                tmpl = paged_entry_array(pc, block_table, rows[sel], qs[sel], tq[sel],
+                                         (tk - tq)[sel], 0, tk[sel])
+            _STEP["fast"][key] = tmpl
+        ent = tmpl.copy()
+        ent["k_addr"] = pc.k_addr
+        ent["v_addr"] = pc.v_addr
+        keep = (kv_cache, block_table)
+        if is_decode:
+            DecodeBatch.from_entries(ent, self.num_heads, self.num_kv_heads, self.head_size,
+                                     query.device, keep=keep).run(query, out, None, self.scale)
+            _count("decode")
+        else:
+            lse = torch.empty((self.num_heads, query.shape[0]), dtype=torch.float32,
+                              device=query.device)
+            VarlenLaunch(ent, True, True, query.device, keep=keep).run(
+                query, out, lse, self.num_kv_heads, self.scale, w)
+            _count("attn")
 
     def _forward_prefill(self, query, out, plan: _Plan) -> None:
         dev = query.device

@@ -22,6 +22,8 @@ from __future__ import annotations
 import ctypes
 from dataclasses import dataclass
 
+import numpy as np
+
 import torch
 
 from . import _lib
@@ -190,9 +192,15 @@ def make_entry(q_start: int, q_len: int, seg: KvSegment, causal_offset: int = 0)
     return e
 
 
+def _nbytes_addr(a) -> tuple[int, int]:
+    if isinstance(a, np.ndarray):
+        return a.nbytes, a.ctypes.data
+    return ctypes.sizeof(a), ctypes.addressof(a)
+
+
 def _upload(arrays, device: torch.device):
-    """Copy ctypes arrays to the device in one asynchronous copy from pinned
-    memory on the current stream.
+    """Copy ctypes or numpy arrays to the device in one asynchronous copy from
+    pinned memory on the current stream.
 
     Returns (device byte tensor, [address of each array on the device]), each
     array 256-byte aligned.  The pinned block comes from torch's caching host
@@ -201,13 +209,65 @@ def _upload(arrays, device: torch.device):
     offs, total = [], 0
     for a in arrays:
         offs.append(total)
-        total += (ctypes.sizeof(a) + 255) & ~255
+        total += (_nbytes_addr(a)[0] + 255) & ~255
     host = torch.empty(max(total, 256), dtype=torch.uint8, pin_memory=True)
     base = host.data_ptr()
     for a, o in zip(arrays, offs):
-        ctypes.memmove(base + o, ctypes.addressof(a), ctypes.sizeof(a))
+        nb, addr = _nbytes_addr(a)
+        ctypes.memmove(base + o, addr, nb)
     dev = host.to(device, non_blocking=True)
     return dev, [dev.data_ptr() + o for o in offs]
+
+
+# hcp_varlen_entry as a numpy record (include/hcp_mi355x.h), for building a
+# whole batch's entries with array operations instead of one object each
+ENTRY_DTYPE = np.dtype({
+    "names": ["q_start", "q_len", "causal_offset", "k_addr", "v_addr", "block_table",
+              "stride_tok", "stride_head", "stride_block", "start", "len", "block_size",
+              "num_blocks"],
+    "formats": ["<i8", "<i8", "<i8", "<u8", "<u8", "<u8", "<i8", "<i8", "<i8", "<i8", "<i8",
+                "<i4", "<i4"],
+    "offsets": [0, 8, 16, 24, 32, 40, 48, 56, 64, 72, 80, 88, 92],
+    "itemsize": 96,
+})
+assert ENTRY_DTYPE.itemsize == ctypes.sizeof(VarlenEntry)
+
+
+def paged_entry_array(pc: "PagedCache", block_table: torch.Tensor, rows, q_start, q_len,
+                      causal_offset, start, length) -> np.ndarray:
+    """Entries over the paged cache for many requests at once: entry i covers
+    query rows [q_start[i], +q_len[i]) and tokens [start[i], +length[i]) of
+    block-table row rows[i].  ``block_table`` is the batch's contiguous int32
+    table on the device; all checks are done once for the batch."""
+    if block_table.dtype != torch.int32 or not block_table.is_contiguous():
+        raise ValueError("block table must be contiguous int32")
+    _check_kv_layout(pc.k_addr, pc.v_addr, pc.stride_tok, pc.stride_head, pc.stride_block,
+                     pc.cache.element_size())
+    if pc.block_size <= 0 or pc.block_size & (pc.block_size - 1):
+        raise ValueError("block_size must be a power of two")
+    rows = np.asarray(rows, dtype=np.int64)
+    start = np.asarray(start, dtype=np.int64)
+    length = np.asarray(length, dtype=np.int64)
+    if (start < 0).any() or (length < 0).any():
+        raise ValueError("negative segment start/length")
+    nblk = (start + length + pc.block_size - 1) // pc.block_size
+    if ((length > 0) & (nblk > block_table.shape[1])).any():
+        raise ValueError("segment extends past the block-table row")
+    a = np.zeros(len(rows), dtype=ENTRY_DTYPE)
+    a["q_start"] = q_start
+    a["q_len"] = q_len
+    a["causal_offset"] = causal_offset
+    a["k_addr"] = pc.k_addr
+    a["v_addr"] = pc.v_addr
+    a["block_table"] = block_table.data_ptr() + rows * block_table.stride(0) * 4
+    a["stride_tok"] = pc.stride_tok
+    a["stride_head"] = pc.stride_head
+    a["stride_block"] = pc.stride_block
+    a["start"] = start
+    a["len"] = length
+    a["block_size"] = pc.block_size
+    a["num_blocks"] = pc.num_blocks if pc.num_blocks < (1 << 31) else 0
+    return a
 
 
 def plan_varlen_tiles(entries: list[VarlenEntry], causal: bool) -> list[tuple[int, int]]:
@@ -233,28 +293,38 @@ class VarlenLaunch:
     stream (or synchronise first).
     """
 
-    def __init__(self, entries: list[VarlenEntry], causal: bool, paged: bool,
-                 device: torch.device):
+    def __init__(self, entries, causal: bool, paged: bool, device: torch.device, keep=None):
+        """``entries``: a list of VarlenEntry, or an ENTRY_DTYPE array (then
+        ``keep`` holds the tensors its addresses point into)."""
         L = _lib.lib()
         self.causal = bool(causal)
         self.paged = bool(paged)
         self.num_entries = len(entries)
-        for e in entries:
-            if (e.kv.block_table != 0) != self.paged:
-                raise ValueError("all entries of a launch must share the KV form")
-        arr = (VarlenEntry * max(self.num_entries, 1))(*entries)
         bm = L.hcp_varlen_block_m(128, _lib.DTYPE_BF16)
-        cap = sum((e.q_len + bm - 1) // bm for e in entries)
+        if isinstance(entries, np.ndarray):
+            if entries.dtype != ENTRY_DTYPE or not entries.flags.c_contiguous:
+                raise ValueError("entry array must be contiguous ENTRY_DTYPE")
+            if ((entries["block_table"] != 0) != self.paged).any():
+                raise ValueError("all entries of a launch must share the KV form")
+            arr = entries if self.num_entries else np.zeros(1, dtype=ENTRY_DTYPE)
+            cap = int(((entries["q_len"] + bm - 1) // bm).sum())
+            self._keep = keep
+        else:
+            for e in entries:
+                if (e.kv.block_table != 0) != self.paged:
+                    raise ValueError("all entries of a launch must share the KV form")
+            arr = (VarlenEntry * max(self.num_entries, 1))(*entries)
+            cap = sum((e.q_len + bm - 1) // bm for e in entries)
+            # the entries point at K/V / cache / block-table storage by
+            # address: hold those tensors for as long as this launch can run
+            self._keep = [getattr(e, "_keep", None) for e in entries]
         tiles = (ctypes.c_int32 * max(2 * cap, 2))()
-        rc = L.hcp_plan_varlen_tiles(ctypes.addressof(arr), self.num_entries,
+        rc = L.hcp_plan_varlen_tiles(_nbytes_addr(arr)[1], self.num_entries,
                                      int(self.causal), bm, ctypes.addressof(tiles), cap)
         _lib.check(rc, "hcp_plan_varlen_tiles")
         self.num_tiles = rc
         self._plan_dev, (self.entries_ptr, self.tiles_ptr) = _upload([arr, tiles], device)
         self.device = device
-        # the entries point at K/V / cache / block-table storage by address:
-        # hold those tensors for as long as this launch can run
-        self._keep = [getattr(e, "_keep", None) for e in entries]
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
             num_kv_heads: int, scale: float, window: int | None = None) -> None:
@@ -371,6 +441,43 @@ class DecodeBatch:
         self.device = device
         # the segments point at K/V / cache / block-table storage by address
         self._keep = [getattr(e, "_keep", None) for e in entries]
+
+    @classmethod
+    def from_entries(cls, entries: np.ndarray, num_heads: int, num_kv_heads: int,
+                     head_dim: int, device: torch.device, split_tokens: int | None = None,
+                     keep=None) -> "DecodeBatch":
+        """One entry per sequence (sequence i = entry i = query row i) given as
+        an ENTRY_DTYPE array; ``keep`` holds the tensors it points into."""
+        if entries.dtype != ENTRY_DTYPE or not entries.flags.c_contiguous:
+            raise ValueError("entry array must be contiguous ENTRY_DTYPE")
+        L = _lib.lib()
+        self = cls.__new__(cls)
+        n = len(entries)
+        self.num_seqs = n
+        self.num_entries = n
+        lens = entries["len"]
+        if split_tokens is None:
+            split_tokens = choose_split_tokens([int(lens.sum())], num_kv_heads)
+        self.split_tokens = split_tokens
+        arr = entries if n else np.zeros(1, dtype=ENTRY_DTYPE)
+        seq_arr = np.arange(max(n, 1), dtype=np.int32)
+        cap = int(((lens + split_tokens - 1) // split_tokens).sum())
+        splits = (DecodeSplit * max(cap, 1))()
+        starts = (ctypes.c_int32 * (n + 1))()
+        rc = L.hcp_plan_decode_splits(arr.ctypes.data, n, seq_arr.ctypes.data, n, 0,
+                                      split_tokens, ctypes.addressof(splits), cap,
+                                      ctypes.addressof(starts))
+        _lib.check(rc, "hcp_plan_decode_splits")
+        self.num_splits = rc
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self._plan_dev, (self.entries_ptr, self.splits_ptr, self.starts_ptr) = _upload(
+            [arr, splits, starts], device)
+        self.ws_bytes = int(L.hcp_decode_workspace_bytes(max(rc, 1), num_heads, head_dim))
+        self.device = device
+        self._keep = keep
+        return self
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
             scale: float, acc: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
