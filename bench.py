@@ -183,6 +183,51 @@ def bench_decode(dev, steps, warmup):
     }
 
 
+def bench_decode_paged(dev, steps, warmup, seqs=64, keys=34000, bs=16, seed=7):
+    """Serving decode with every key in the paged cache (no peer): 64 requests
+    of 34000 keys, the layer's cache [nb, 4, 16, 256] bf16 of 4.46 GB (past
+    the 4 GiB of 32-bit buffer offsets, so the 64-bit load path).  ``ms`` is
+    the split-KV kernel pair; ``forward_ms`` the backend's whole per-layer
+    call (HcpRingAttentionImpl.forward: planning + launch), metadata reused
+    across calls as vLLM does across the layers of a step."""
+    import types
+
+    from hcp_vllm_plugin_amd import ring_backend as rb
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    nbk = -(-keys // bs)
+    nb = seqs * nbk + 4
+    cache = torch.empty(nb, HKV, bs, 2 * D, dtype=torch.bfloat16, device=dev)
+    cache.normal_(generator=gen)
+    perm = torch.randperm(nb, device=dev, generator=gen)[: seqs * nbk].to(torch.int32)
+    bt = perm.view(seqs, nbk).contiguous()
+    q = torch.randn(seqs, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    meta = types.SimpleNamespace(
+        num_actual_tokens=seqs,
+        query_start_loc=torch.arange(seqs + 1, dtype=torch.int32, device=dev),
+        seq_lens=torch.full((seqs,), keys, dtype=torch.int32, device=dev), block_table=bt)
+    impl = rb.HcpRingAttentionImpl(H, D, SCALE, HKV)
+    layer = types.SimpleNamespace(layer_name="bench")
+    out = torch.empty_like(q)
+    fwd = lambda: impl.forward(layer, q, None, None, cache, meta, out)
+    ms_fwd = timed(fwd, steps, warmup)
+    from hcp_vllm_plugin_amd.varlen import DecodeBatch, PagedCache, paged_entry_array
+
+    pc = PagedCache.from_tensor(cache)
+    ent = paged_entry_array(pc, bt, range(seqs), range(seqs), 1, 0, [0] * seqs, [keys] * seqs)
+    batch = DecodeBatch.from_entries(ent, H, HKV, D, dev, keep=(cache, bt))
+    ms = timed(lambda: batch.run(q, out, None, SCALE), steps, warmup)
+    byts = seqs * keys * HKV * D * 2 * 2 + seqs * H * D * 2 * 2
+    del cache
+    return {
+        "workload": (f"serving decode, all keys paged: {seqs} requests x {keys} keys, cache "
+                     f"[{nb},4,16,256] bf16 ({nb * HKV * bs * 2 * D * 2 / 1e9:.2f} GB)"),
+        "ms": round(ms, 4), "gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "bytes": byts,
+        "forward_ms": round(ms_fwd, 4),
+    }
+
+
 def timed(fn, steps, warmup):
     """Mean ms of fn() over `steps` runs after `warmup`, HIP events on the
     current stream."""
@@ -566,7 +611,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
-                                       "kvwrite", "ingest", "ringdec", "window", "copy"),
+                                       "kvwrite", "ingest", "ringdec", "window", "pdecode",
+                                       "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -593,6 +639,9 @@ def main():
     if args.part == "ingest":
         print(json.dumps(bench_peer_ingest(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "pdecode":
+        print(json.dumps(bench_decode_paged(dev, args.steps, args.warmup)), flush=True)
+        return
     if args.part == "window":
         print(json.dumps(bench_sliding_window(dev, args.steps, args.warmup)), flush=True)
         return
@@ -618,6 +667,7 @@ def main():
         extra["peer_ingest"] = bench_peer_ingest(dev, args.steps, args.warmup)
         extra["ring_decode_hop"] = bench_ring_decode_hop(dev, args.steps, args.warmup)
         extra["sliding_window"] = bench_sliding_window(dev, args.steps, args.warmup)
+        extra["decode_paged"] = bench_decode_paged(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 

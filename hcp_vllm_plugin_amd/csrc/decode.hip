@@ -53,7 +53,7 @@ struct DecShared {
 };
 
 template <int D, typename T, bool PAGED>
-__device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, int sp,
+__device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in, int sp,
                                                   const hcp_varlen_entry& e,
                                                   const hcp_decode_split& spl,
                                                   char (*bufE)[2 * DecShared<D>::CHB],
@@ -81,6 +81,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
   const int G = p.group;
+  // the KV head is workgroup-uniform: keep every address built from it in
+  // SGPRs (buffer descriptors from VGPR values become waterfall loops)
+  const int kvh = __builtin_amdgcn_readfirstlane(kvh_in);
   KvAddr kva;
   kva.init(e.kv);
   const int64_t kb = spl.key_begin, ke = spl.key_end;
@@ -112,6 +115,7 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
   // instruction reads KPI whole rows (1 KB), streamed past the caches.
   const int kr = lane / CPR, sl = lane % CPR;
   const int64_t rowb_g = kva.stride_tok * 2;
+  // (contiguous segments; paged ones are issued by the loop further down)
   auto issue = [&](int64_t k0, HCP_LDS_PTR(char) dst) __attribute__((always_inline)) {
     if constexpr (!PAGED) {
       const int64_t rows = ke - k0;  // >= 1 valid rows in this chunk
@@ -132,22 +136,6 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rv, reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16, off, 0, 0,
             kStreamAux);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NLD; ++j) {
-        const int row = j * KPI + kr;
-        int64_t key = k0 + row;
-        key = key < ke ? key : ke - 1;  // rows past the split: masked below
-        const int64_t o = (kva.offset<true>(key, kvh) + 8 * (sl ^ (row % CPR))) * 2;
-        __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const __attribute__((address_space(1))) void*>(
-                reinterpret_cast<uintptr_t>(kva.k + o)),
-            reinterpret_cast<HCP_LDS_PTR(void)>(dst + j * 1024), 16, 0, kStreamAux);
-        __builtin_amdgcn_global_load_lds(
-            reinterpret_cast<const __attribute__((address_space(1))) void*>(
-                reinterpret_cast<uintptr_t>(kva.v + o)),
-            reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16, 0, kStreamAux);
       }
     }
   };
@@ -246,7 +234,101 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh, i
   // issued (into the other buffer) are outstanding: its own DMA into the
   // buffer it reads has landed.  Buffers are wave-private, so no barrier.
   int64_t ci = wave;
-  if (ci < nchunks) {
+  // Paged segments: the lane's block ids are fetched one chunk ahead of the
+  // chunk's DMA, so looking them up never waits on the DMA in flight.  When
+  // the cache spans less than 4 GiB from this head's base the DMA is a
+  // bounds-checked buffer load over one descriptor for the whole cache (a
+  // block id past the cache reads zeros); otherwise a global load with a
+  // 64-bit address.
+  if constexpr (PAGED) {
+    const int64_t blockb = kva.stride_block * 2;
+    const uint64_t span = static_cast<uint64_t>(e.kv.num_blocks) * static_cast<uint64_t>(blockb);
+    const bool pbuf = e.kv.num_blocks > 0 && span < (uint64_t{1} << 32);
+    if (ci < nchunks) {
+      const int64_t hb = static_cast<int64_t>(kvh) * kva.stride_head * 2;
+      const int nrec =
+          __builtin_amdgcn_readfirstlane(pbuf ? static_cast<int>(static_cast<uint32_t>(span)) : 0);
+      // the bases are wave-uniform; say so, or the descriptors land in
+      // VGPRs and every buffer load becomes a waterfall loop
+      auto uniform_ptr = [](const char* ptr) __attribute__((always_inline)) {
+        const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+        const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+        return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
+      };
+      const __amdgpu_buffer_rsrc_t rk =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kva.k + hb), 0, nrec, kBufWord3);
+      const __amdgpu_buffer_rsrc_t rv =
+          __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kva.v + hb), 0, nrec, kBufWord3);
+      uint32_t idA[NLD], idB[NLD];
+      auto fetch_ids = [&](int64_t k0, uint32_t (&ids)[NLD]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+          int64_t key = k0 + j * KPI + kr;
+          key = key < ke ? key : ke - 1;  // rows past the split: masked
+          ids[j] = static_cast<uint32_t>(kva.bt[(kva.start + key) >> kva.bs_shift]);
+        }
+      };
+      // one chunk's DMA; BUF (compile-time) picks the load form
+      auto issue_p = [&](auto buf, int64_t k0, const uint32_t (&ids)[NLD], HCP_LDS_PTR(char) dst)
+          __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+          const int row = j * KPI + kr;
+          int64_t key = k0 + row;
+          key = key < ke ? key : ke - 1;
+          const int64_t x = kva.start + key;
+          const int64_t inb = (x & kva.bs_mask) * rowb_g + 16 * (sl ^ (row % CPR));
+          if constexpr (decltype(buf)::value) {
+            const uint32_t off = ids[j] * static_cast<uint32_t>(blockb) + static_cast<uint32_t>(inb);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, reinterpret_cast<HCP_LDS_PTR(void)>(dst + j * 1024), 16,
+                static_cast<int>(off), 0, 0, kStreamAux);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16,
+                static_cast<int>(off), 0, 0, kStreamAux);
+          } else {
+            const int64_t o = static_cast<int64_t>(ids[j]) * blockb + hb + inb;
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const __attribute__((address_space(1))) void*>(
+                    reinterpret_cast<uintptr_t>(kva.k + o)),
+                reinterpret_cast<HCP_LDS_PTR(void)>(dst + j * 1024), 16, 0, kStreamAux);
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const __attribute__((address_space(1))) void*>(
+                    reinterpret_cast<uintptr_t>(kva.v + o)),
+                reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16, 0, kStreamAux);
+          }
+        }
+      };
+      // per step: fetch the ids of chunk ci+8, issue chunk ci+4 (its ids
+      // fetched a step ago), wait until only those 3*NLD loads are
+      // outstanding -- chunk ci has landed -- and compute it
+      auto run_loop = [&](auto buf) __attribute__((always_inline)) {
+        fetch_ids(kb + ci * kDecChunk, idA);
+        fetch_ids(next_k0(ci + 4), idB);
+        issue_p(buf, kb + ci * kDecChunk, idA, be);
+        while (true) {
+          fetch_ids(next_k0(ci + 8), idA);
+          issue_p(buf, next_k0(ci + 4), idB, bo);
+          wait_vmcnt<3 * NLD>();
+          compute(kb + ci * kDecChunk, be);
+          ci += 4;
+          if (ci >= nchunks) break;
+          fetch_ids(next_k0(ci + 8), idB);
+          issue_p(buf, next_k0(ci + 4), idA, be);
+          wait_vmcnt<3 * NLD>();
+          compute(kb + ci * kDecChunk, bo);
+          ci += 4;
+          if (ci >= nchunks) break;
+        }
+      };
+      if (pbuf)
+        run_loop(std::true_type{});
+      else
+        run_loop(std::false_type{});
+    }
+  }
+  if (!PAGED && ci < nchunks) {
     issue(kb + ci * kDecChunk, be);
     while (true) {
       issue(next_k0(ci + 4), bo);
