@@ -5,9 +5,12 @@ Workload (the headline prefill step): Qwen2.5-7B attention shape (28 query
 heads, 4 KV heads, head_dim 128, scale 1/sqrt(128)), bf16, one request, one
 layer: 8192 local query tokens causal over 8192 local keys (kernel-frame
 offset 0: local keys sit at global 8192..16383, after the peer chunk) plus
-8192 transient peer keys non-causal, then the LSE merge.  Seeded N(0,1)
-inputs with 4 of 128 K channels scaled x8 (logit outliers).  A step is
-local pass + peer pass + merge; inputs are resident in HBM before timing.
+8192 transient peer keys non-causal, merged by LSE.  Seeded N(0,1) inputs
+with 4 of 128 K channels scaled x8 (logit outliers).  A step is the peer
+pass, then the local pass that merges the peer result into the output in the
+same launch (bit for bit the local pass + peer pass + merge_attn_states of
+the reference's forward, whose separate timing is reported as "two_step");
+inputs are resident in HBM before timing.
 
 Also measured in the same run (reported under "decode"): batch-64 split-KV
 decode -- 64 sequences, one query token each, a 32768-token contiguous peer
@@ -75,8 +78,13 @@ def prefill_inputs(dev, seed=1, n=8192):
     return tuple(cast(t).to(dev) for t in (q, kl, vl, kp, vp))
 
 
-def bench_prefill(dev, steps, warmup):
-    from hcp_vllm_plugin_amd import merge_attn_states, ring_attn_with_lse
+def bench_prefill(dev, steps, warmup, two_step=True):
+    """The headline step as the backend runs it: the peer pass, then the local
+    causal pass that merges the peer result into the output in the same launch
+    (hcp_attn_fwd_lse_merge; equal bit for bit to local pass + peer pass +
+    merge_attn_states).  The two-step form's local pass and merge kernel are
+    timed as well, for comparison."""
+    from hcp_vllm_plugin_amd import merge_attn_states, ring_attn_merged, ring_attn_with_lse
 
     n = 8192
     q, kl, vl, kp, vp = prefill_inputs(dev)
@@ -85,29 +93,32 @@ def bench_prefill(dev, steps, warmup):
     def step(ev=None):
         if ev is not None:
             ev[0].record()
-        o_loc, lse_loc = ring_attn_with_lse(q, kl, vl, SCALE, 0)
-        if ev is not None:
-            ev[1].record()
         o_peer, lse_peer = ring_attn_with_lse(q, kp, vp, SCALE, None)
         if ev is not None:
-            ev[2].record()
-        merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc)
+            ev[1].record()
+        ring_attn_merged(q, kl, vl, SCALE, 0, o_peer, lse_peer, output=out)
         if ev is not None:
-            ev[3].record()
+            ev[2].record()
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    t_loc = [e[0].elapsed_time(e[1]) for e in evs]
-    t_peer = [e[1].elapsed_time(e[2]) for e in evs]
-    t_merge = [e[2].elapsed_time(e[3]) for e in evs]
+    t_peer = [e[0].elapsed_time(e[1]) for e in evs]
+    t_loc = [e[1].elapsed_time(e[2]) for e in evs]
+    # the two-step form: plain local pass and the separate merge kernel
+    t_loc_plain = t_merge = float("nan")
+    if two_step:
+        t_loc_plain = timed(lambda: ring_attn_with_lse(q, kl, vl, SCALE, 0), steps, warmup)
+        o_l, l_l = ring_attn_with_lse(q, kl, vl, SCALE, 0)
+        o_p, l_p = ring_attn_with_lse(q, kp, vp, SCALE, None)
+        t_merge = timed(lambda: merge_attn_states(out, o_p, l_p, o_l, l_l), steps, warmup)
     f_loc = 4 * D * H * causal_pairs(n, n, 0)
     f_peer = 4 * D * H * n * n
     merge_bytes = 3 * n * H * D * 2 + 2 * n * H * 4
@@ -117,7 +128,8 @@ def bench_prefill(dev, steps, warmup):
         "flops": f_loc + f_peer,
         "local": {"ms": statistics.mean(t_loc), "flops": f_loc},
         "peer": {"ms": statistics.mean(t_peer), "flops": f_peer},
-        "merge": {"ms": statistics.mean(t_merge), "bytes": merge_bytes},
+        "local_plain": {"ms": t_loc_plain, "flops": f_loc},
+        "merge": {"ms": t_merge, "bytes": merge_bytes},
     }
 
 
@@ -285,25 +297,29 @@ def bench_varlen(dev, steps, warmup, seed=2, nreq=16, bs=16):
     o_loc, o_peer, out = (torch.empty_like(q) for _ in range(3))
     lse_loc = torch.empty(H, tq, device=dev)
     lse_peer = torch.empty(H, tq, device=dev)
-    t_loc = timed(lambda: l_launch.run(q, o_loc, lse_loc, HKV, SCALE), steps, warmup)
     t_peer = timed(lambda: p_launch.run(q, o_peer, lse_peer, HKV, SCALE), steps, warmup)
+    t_loc = timed(lambda: l_launch.run(q, out, None, HKV, SCALE, acc=(o_peer, lse_peer)),
+                  steps, warmup)
+    # the two-step form: plain local launch and the separate merge
+    t_loc_plain = timed(lambda: l_launch.run(q, o_loc, lse_loc, HKV, SCALE), steps, warmup)
     t_merge = timed(lambda: merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc),
                     steps, warmup)
     pairs_l = sum(causal_pairs(l, l, 0) for l in loc)
     pairs_p = sum(l * p for l, p in zip(loc, pre))
     f_l, f_p = 4 * D * H * pairs_l, 4 * D * H * pairs_p
-    t = t_loc + t_peer + t_merge
+    t = t_loc + t_peer
     tf = (f_l + f_p) / (t * 1e-3) / 1e12
     return {
         "workload": (f"varlen prefill: {nreq} requests, local U[512,4096] causal over a paged "
-                     f"[nb,4,16,256] cache + peer 16*U[64,1024] contiguous, one launch per "
-                     f"segment kind, then the merge"),
+                     f"[nb,4,16,256] cache + peer 16*U[64,1024] contiguous: the peer launch, "
+                     f"then the local launch merging the peer result into the output"),
         "query_tokens": tq, "peer_tokens": tp,
         "ms": round(t, 4), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-        "local_paged": {"ms": round(t_loc, 4),
-                        "tflops": round(f_l / (t_loc * 1e-3) / 1e12, 2)},
+        "local_paged_merged": {"ms": round(t_loc, 4),
+                               "tflops": round(f_l / (t_loc * 1e-3) / 1e12, 2)},
         "peer": {"ms": round(t_peer, 4), "tflops": round(f_p / (t_peer * 1e-3) / 1e12, 2)},
-        "merge_ms": round(t_merge, 4),
+        "two_step": {"local_paged_ms": round(t_loc_plain, 4), "merge_ms": round(t_merge, 4),
+                     "ms": round(t_loc_plain + t_peer + t_merge, 4)},
         "tflop": round((f_l + f_p) / 1e12, 3),
     }
 
@@ -471,8 +487,9 @@ def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
     head_dim 128), bf16: 65536 local query tokens causal over local keys
     (global offset 65536: the peer chunk comes first) + 65536 peer keys,
     processed as 8 query chunks of 8192; chunk c attends local keys
-    [0, 8192(c+1)) at offset 8192c, then all peer keys, then the LSE merge."""
-    from hcp_vllm_plugin_amd import merge_attn_states, ring_attn_with_lse
+    [0, 8192(c+1)) at offset 8192c and all peer keys: the peer pass, then the
+    local causal pass merging the peer result into the chunk's output."""
+    from hcp_vllm_plugin_amd import ring_attn_merged, ring_attn_with_lse
 
     h, hkv = 64, 8
     dgen = torch.Generator(device=dev).manual_seed(seed)
@@ -487,8 +504,6 @@ def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
     vp = torch.randn(n, hkv, D, generator=dgen, device=dev).to(torch.bfloat16)
     out = torch.empty_like(q)
     nchunk = n // chunk
-    t_attn = [0.0]
-    t_merge = [0.0]
 
     def step(ev=None):
         for c in range(nchunk):
@@ -498,12 +513,11 @@ def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
             e2 = torch.cuda.Event(enable_timing=True)
             if ev is not None:
                 e0.record()
-            o_l, l_l = ring_attn_with_lse(qc, kl[:chunk * (c + 1)], vl[:chunk * (c + 1)],
-                                          SCALE, chunk * c)
             o_p, l_p = ring_attn_with_lse(qc, kp, vp, SCALE, None)
             if ev is not None:
                 e1.record()
-            merge_attn_states(out[c * chunk:(c + 1) * chunk], o_p, l_p, o_l, l_l)
+            ring_attn_merged(qc, kl[:chunk * (c + 1)], vl[:chunk * (c + 1)], SCALE, chunk * c,
+                             o_p, l_p, output=out[c * chunk:(c + 1) * chunk])
             if ev is not None:
                 e2.record()
                 ev.append((e0, e1, e2))
@@ -517,17 +531,18 @@ def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
         step(evs)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    attn = sum(a.elapsed_time(b) for a, b, _ in evs) / steps
-    merge = sum(b.elapsed_time(c) for _, b, c in evs) / steps
+    peer = sum(a.elapsed_time(b) for a, b, _ in evs) / steps
+    local = sum(b.elapsed_time(c) for _, b, c in evs) / steps
     pairs = sum(causal_pairs(chunk, chunk * (c + 1), chunk * c) for c in range(nchunk)) + n * n
     flops = 4 * D * h * pairs
     tf = flops / (wall * 1e-3) / 1e12
     return {
         "workload": ("Llama-3-70B attention shape (64/8 heads, head_dim 128) bf16: 65536 local "
-                     "causal + 65536 peer keys, 8 query chunks of 8192 with the LSE merge"),
+                     "causal + 65536 peer keys, 8 query chunks of 8192, each local pass "
+                     "merging its chunk's peer result"),
         "ms": round(wall, 3), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
-        "attn_ms": round(attn, 3), "merge_ms": round(merge, 3),
-        "merge_overhead": round(merge / wall, 4), "tflop": round(flops / 1e12, 2),
+        "peer_ms": round(peer, 3), "local_merged_ms": round(local, 3),
+        "tflop": round(flops / 1e12, 2),
     }
 
 
@@ -608,6 +623,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-two-step", action="store_true",
+                    help="skip timing the unfused local pass + merge (kernel traces of the step)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
@@ -654,7 +671,7 @@ def main():
     if args.part == "llama70b":
         print(json.dumps(bench_llama70b(dev, 2, 1)), flush=True)
         return
-    pre = bench_prefill(dev, args.steps, args.warmup)
+    pre = bench_prefill(dev, args.steps, args.warmup, two_step=not args.no_two_step)
     if args.part == "prefill":
         print(json.dumps(pre), flush=True)
         return
@@ -674,6 +691,7 @@ def main():
     value = pre["flops"] / (pre["ms_per_step"] * 1e-3) / 1e12
     peer_tf = pre["peer"]["flops"] / (pre["peer"]["ms"] * 1e-3) / 1e12
     loc_tf = pre["local"]["flops"] / (pre["local"]["ms"] * 1e-3) / 1e12
+    locp_tf = pre["local_plain"]["flops"] / (pre["local_plain"]["ms"] * 1e-3) / 1e12
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -688,7 +706,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1), 4 of 128 K channels x8",
         "config": {
-            "workload": "ring prefill step: 8192 local causal + 8192 peer non-causal + LSE merge",
+            "workload": ("ring prefill step: 8192 peer keys non-causal, then 8192 local causal "
+                         "with the LSE merge in the same launch"),
             "q_heads": H, "kv_heads": HKV, "head_dim": D,
             "local_tokens": 8192, "peer_tokens": 8192, "causal_frame_offset": 0,
             "parallelism": "single GPU",
@@ -703,14 +722,21 @@ def main():
             "traffic": traffic.get("fa_fwd_peer", {}).get("bytes"),
         },
         "kernels": {
-            "local_causal": {"ms": round(pre["local"]["ms"], 4), "tflops": round(loc_tf, 2),
-                             "frac": round(loc_tf / PEAK_BF16_TFLOPS, 4),
-                             "traffic": traffic.get("fa_fwd_local", {}).get("bytes")},
+            "local_causal_merged": {"ms": round(pre["local"]["ms"], 4),
+                                    "tflops": round(loc_tf, 2),
+                                    "frac": round(loc_tf / PEAK_BF16_TFLOPS, 4),
+                                    "traffic": traffic.get("fa_fwd_local", {}).get("bytes")},
             "peer": {"ms": round(pre["peer"]["ms"], 4), "tflops": round(peer_tf, 2),
                      "frac": round(peer_tf / PEAK_BF16_TFLOPS, 4)},
-            "merge": {"ms": round(pre["merge"]["ms"], 4),
-                      "gbs": round(pre["merge"]["bytes"] / (pre["merge"]["ms"] * 1e-3) / 1e9, 1),
-                      "traffic": traffic.get("merge", {}).get("bytes")},
+            "two_step": None if math.isnan(pre["merge"]["ms"]) else {
+                         "local_causal_ms": round(pre["local_plain"]["ms"], 4),
+                         "local_causal_tflops": round(locp_tf, 2),
+                         "merge_ms": round(pre["merge"]["ms"], 4),
+                         "merge_gbs": round(pre["merge"]["bytes"] / (pre["merge"]["ms"] * 1e-3)
+                                            / 1e9, 1),
+                         "merge_traffic": traffic.get("merge", {}).get("bytes"),
+                         "step_ms": round(pre["local_plain"]["ms"] + pre["peer"]["ms"]
+                                          + pre["merge"]["ms"], 4)},
         },
         "cpu_baseline": cpu,
     }

@@ -18,11 +18,12 @@ Importing the package does not import vLLM; ``register()`` does.
 from __future__ import annotations
 
 from .merge import merge_attn_states, merge_pair
-from .ring_attn import ring_attn_with_lse
+from .ring_attn import ring_attn_merged, ring_attn_with_lse
 
 __all__ = [
     "register",
     "ring_attn_with_lse",
+    "ring_attn_merged",
     "merge_attn_states",
     "merge_pair",
     "BACKEND_PATH",

@@ -45,9 +45,11 @@ EXPORTED_SYMBOLS = (
     "hcp_abi_version",
     "hcp_last_error",
     "hcp_attn_fwd_lse",
+    "hcp_attn_fwd_lse_merge",
     "hcp_varlen_block_m",
     "hcp_plan_varlen_tiles",
     "hcp_attn_fwd_varlen",
+    "hcp_attn_fwd_varlen_merge",
     "hcp_plan_decode_splits",
     "hcp_decode_workspace_bytes",
     "hcp_decode_splitkv",
@@ -56,7 +58,7 @@ EXPORTED_SYMBOLS = (
     "hcp_reshape_and_cache",
 )
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class KvSegment(ctypes.Structure):
@@ -133,6 +135,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
         _F, _I32, _I64, _I32, _I32, _P,
     ]
+    lib.hcp_attn_fwd_lse_merge.restype = ctypes.c_int
+    lib.hcp_attn_fwd_lse_merge.argtypes = [
+        _P, _P, _P, _P, _P, _I64, _I64, _I32, _I32, _I32,
+        _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+        _F, _I32, _I64, _I32, _P, _I64, _I64, _P, _I64, _I32, _I32, _P,
+    ]
     lib.hcp_varlen_block_m.restype = ctypes.c_int
     lib.hcp_varlen_block_m.argtypes = [_I32, _I32]
     lib.hcp_plan_varlen_tiles.restype = ctypes.c_int
@@ -141,6 +149,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_attn_fwd_varlen.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
         _P, _I32, _P, _I32, _I32, _I32, _I32, _F, _I32, _I32, _I32, _I32, _P,
+    ]
+    lib.hcp_attn_fwd_varlen_merge.restype = ctypes.c_int
+    lib.hcp_attn_fwd_varlen_merge.argtypes = [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+        _P, _I32, _P, _I32, _I32, _I32, _I32, _F, _I32, _I32, _I32,
+        _P, _I64, _I64, _P, _I64, _I32, _I32, _P,
     ]
     lib.hcp_plan_decode_splits.restype = ctypes.c_int
     lib.hcp_plan_decode_splits.argtypes = [_P, _I32, _P, _I32, _I32, _I32, _P, _I32, _P]

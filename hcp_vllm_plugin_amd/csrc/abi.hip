@@ -59,6 +59,36 @@ int check_segment(const hcp_kv_segment& s, int32_t hd, const char* who, int idx)
   return HCP_OK;
 }
 
+// Optional partial state merged into an attention pass's result.
+struct AccArgs {
+  const void* o;
+  int64_t stride_tok, stride_head;
+  const float* lse;
+  int64_t lse_stride_head;
+  int32_t prefix;
+};
+
+int check_acc(const AccArgs& a, const char* who) {
+  if (!a.o || !a.lse) return fail(HCP_EINVAL, "%s: null merge partial out/lse", who);
+  if (!aligned16(a.o)) return fail(HCP_EINVAL, "%s: merge partial not 16-byte aligned", who);
+  if ((a.stride_tok | a.stride_head) % 8)
+    return fail(HCP_EINVAL, "%s: merge partial strides must be multiples of 8 elements", who);
+  if (a.stride_tok <= 0 || a.stride_tok >= (int64_t{1} << 24))
+    return fail(HCP_EUNSUPPORTED, "%s: merge partial token stride must be in (0, 2^24) elements",
+                who);
+  return HCP_OK;
+}
+
+void set_acc(hcp::FwdParams& p, const AccArgs* a) {
+  if (!a) return;
+  p.acc_o = a->o;
+  p.acc_stride_tok = a->stride_tok;
+  p.acc_stride_head = a->stride_head;
+  p.acc_lse = a->lse;
+  p.acc_lse_stride_head = a->lse_stride_head;
+  p.acc_prefix = a->prefix != 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -67,19 +97,20 @@ int hcp_abi_version(void) { return HCP_ABI_VERSION; }
 
 const char* hcp_last_error(void) { return g_err; }
 
-int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, float* lse,
-                     int64_t tq, int64_t tk, int32_t num_heads, int32_t num_kv_heads,
-                     int32_t head_dim, int64_t q_stride_tok, int64_t q_stride_head,
-                     int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
-                     int64_t v_stride_head, int64_t o_stride_tok, int64_t o_stride_head,
-                     int64_t lse_stride_head, float scale, int32_t causal,
-                     int64_t causal_offset, int32_t window, int32_t dtype, void* stream) {
-  const char* who = "hcp_attn_fwd_lse";
+static int fwd_lse_impl(const char* who, const void* q, const void* k, const void* v, void* out,
+                        float* lse, int64_t tq, int64_t tk, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int64_t q_stride_tok,
+                        int64_t q_stride_head, int64_t k_stride_tok, int64_t k_stride_head,
+                        int64_t v_stride_tok, int64_t v_stride_head, int64_t o_stride_tok,
+                        int64_t o_stride_head, int64_t lse_stride_head, float scale,
+                        int32_t causal, int64_t causal_offset, int32_t window, int32_t dtype,
+                        void* stream, const AccArgs* acc) {
   int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
   if (rc) return rc;
   if (tq < 0 || tk < 0) return fail(HCP_EINVAL, "%s: negative tq/tk", who);
   if (tq == 0) return HCP_OK;
-  if (!q || !out || !lse) return fail(HCP_EINVAL, "%s: null q/out/lse", who);
+  if (!q || !out || (!lse && !acc)) return fail(HCP_EINVAL, "%s: null q/out/lse", who);
+  if (acc && (rc = check_acc(*acc, who))) return rc;
   if (tk > 0 && (!k || !v)) return fail(HCP_EINVAL, "%s: null k/v", who);
   if (!aligned16(q) || !aligned16(out) || (tk > 0 && (!aligned16(k) || !aligned16(v))))
     return fail(HCP_EINVAL, "%s: q/k/v/out must be 16-byte aligned", who);
@@ -118,9 +149,41 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, flo
     return fail(HCP_EUNSUPPORTED, "%s: k and v must share strides", who);
   if (k_stride_tok <= 0 || k_stride_tok >= (int64_t{1} << 24))
     return fail(HCP_EUNSUPPORTED, "%s: k token stride must be in (0, 2^24) elements", who);
+  set_acc(p, acc);
   hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, false, false,
                                  static_cast<hipStream_t>(stream));
   return launch_status(e, who);
+}
+
+int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out, float* lse,
+                     int64_t tq, int64_t tk, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int64_t q_stride_tok, int64_t q_stride_head,
+                     int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
+                     int64_t v_stride_head, int64_t o_stride_tok, int64_t o_stride_head,
+                     int64_t lse_stride_head, float scale, int32_t causal,
+                     int64_t causal_offset, int32_t window, int32_t dtype, void* stream) {
+  return fwd_lse_impl("hcp_attn_fwd_lse", q, k, v, out, lse, tq, tk, num_heads, num_kv_heads,
+                      head_dim, q_stride_tok, q_stride_head, k_stride_tok, k_stride_head,
+                      v_stride_tok, v_stride_head, o_stride_tok, o_stride_head, lse_stride_head,
+                      scale, causal, causal_offset, window, dtype, stream, nullptr);
+}
+
+int hcp_attn_fwd_lse_merge(const void* q, const void* k, const void* v, void* out, float* lse,
+                           int64_t tq, int64_t tk, int32_t num_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int64_t q_stride_tok, int64_t q_stride_head,
+                           int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
+                           int64_t v_stride_head, int64_t o_stride_tok, int64_t o_stride_head,
+                           int64_t lse_stride_head, float scale, int32_t causal,
+                           int64_t causal_offset, int32_t window, const void* acc_out,
+                           int64_t acc_stride_tok, int64_t acc_stride_head,
+                           const float* acc_lse, int64_t acc_lse_stride_head,
+                           int32_t acc_is_prefix, int32_t dtype, void* stream) {
+  const AccArgs acc{acc_out, acc_stride_tok, acc_stride_head, acc_lse, acc_lse_stride_head,
+                    acc_is_prefix};
+  return fwd_lse_impl("hcp_attn_fwd_lse_merge", q, k, v, out, lse, tq, tk, num_heads,
+                      num_kv_heads, head_dim, q_stride_tok, q_stride_head, k_stride_tok,
+                      k_stride_head, v_stride_tok, v_stride_head, o_stride_tok, o_stride_head,
+                      lse_stride_head, scale, causal, causal_offset, window, dtype, stream, &acc);
 }
 
 int hcp_varlen_block_m(int32_t head_dim, int32_t dtype) {
@@ -165,19 +228,21 @@ int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries, 
   return n;
 }
 
-int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok, int64_t q_stride_head, void* out,
-                        int64_t o_stride_tok, int64_t o_stride_head, float* lse,
-                        int64_t lse_stride_head, const hcp_varlen_entry* entries,
-                        int32_t num_entries, const int32_t* tiles, int32_t num_tiles,
-                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
-                        int32_t causal, int32_t window, int32_t paged, int32_t dtype,
-                        void* stream) {
-  const char* who = "hcp_attn_fwd_varlen";
+static int fwd_varlen_impl(const char* who, const void* q, int64_t q_stride_tok,
+                           int64_t q_stride_head, void* out, int64_t o_stride_tok,
+                           int64_t o_stride_head, float* lse, int64_t lse_stride_head,
+                           const hcp_varlen_entry* entries, int32_t num_entries,
+                           const int32_t* tiles, int32_t num_tiles, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, float scale, int32_t causal,
+                           int32_t window, int32_t paged, int32_t dtype, void* stream,
+                           const AccArgs* acc) {
   int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
   if (rc) return rc;
   if (num_entries < 0 || num_tiles < 0) return fail(HCP_EINVAL, "%s: negative counts", who);
   if (num_tiles == 0) return HCP_OK;
-  if (!q || !out || !lse || !entries || !tiles) return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (!q || !out || (!lse && !acc) || !entries || !tiles)
+    return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (acc && (rc = check_acc(*acc, who))) return rc;
   if (!aligned16(q) || !aligned16(out)) return fail(HCP_EINVAL, "%s: q/out not 16-byte aligned", who);
   if ((q_stride_tok | q_stride_head | o_stride_tok | o_stride_head) % 8)
     return fail(HCP_EINVAL, "%s: strides must be multiples of 8 elements", who);
@@ -201,9 +266,41 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;
   p.scale_log2 = scale * hcp::kLog2e;
+  set_acc(p, acc);
   hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, paged != 0, true,
                                  static_cast<hipStream_t>(stream));
   return launch_status(e, who);
+}
+
+int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok, int64_t q_stride_head, void* out,
+                        int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+                        int64_t lse_stride_head, const hcp_varlen_entry* entries,
+                        int32_t num_entries, const int32_t* tiles, int32_t num_tiles,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                        int32_t causal, int32_t window, int32_t paged, int32_t dtype,
+                        void* stream) {
+  return fwd_varlen_impl("hcp_attn_fwd_varlen", q, q_stride_tok, q_stride_head, out,
+                         o_stride_tok, o_stride_head, lse, lse_stride_head, entries, num_entries,
+                         tiles, num_tiles, num_heads, num_kv_heads, head_dim, scale, causal,
+                         window, paged, dtype, stream, nullptr);
+}
+
+int hcp_attn_fwd_varlen_merge(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                              void* out, int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+                              int64_t lse_stride_head, const hcp_varlen_entry* entries,
+                              int32_t num_entries, const int32_t* tiles, int32_t num_tiles,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              float scale, int32_t causal, int32_t window, int32_t paged,
+                              const void* acc_out, int64_t acc_stride_tok,
+                              int64_t acc_stride_head, const float* acc_lse,
+                              int64_t acc_lse_stride_head, int32_t acc_is_prefix, int32_t dtype,
+                              void* stream) {
+  const AccArgs acc{acc_out, acc_stride_tok, acc_stride_head, acc_lse, acc_lse_stride_head,
+                    acc_is_prefix};
+  return fwd_varlen_impl("hcp_attn_fwd_varlen_merge", q, q_stride_tok, q_stride_head, out,
+                         o_stride_tok, o_stride_head, lse, lse_stride_head, entries, num_entries,
+                         tiles, num_tiles, num_heads, num_kv_heads, head_dim, scale, causal,
+                         window, paged, dtype, stream, &acc);
 }
 
 int hcp_plan_decode_splits(const hcp_varlen_entry* entries, int32_t num_entries,

@@ -755,26 +755,106 @@ fa_fwd_kernel(FwdParams p) {
 
   // ---- epilogue ----
   const float l_tot = l_run + __shfl_xor(l_run, 32);
+  // Merge path: this wave's 32 rows of the partial state are fetched whole
+  // (coalesced) into the wave's share of the tile buffers, free since the
+  // loop's last barrier.  Load instruction i fills bytes [i*1024, +1024) of
+  // the share: lane l writes row i*RPL + l/CPR, 16-byte slot l%CPR, which
+  // holds the row's chunk (l%CPR) ^ (row & (CPR-1)), so the per-lane 8-byte
+  // reads below are at most two-way bank conflicted.  Rows past q_len lie
+  // beyond the descriptor's range and read as zeros.
+  constexpr int CPR = ROWB / 16;    // 16-byte chunks per row
+  constexpr int RPL = 1024 / ROWB;  // rows per load instruction
+  static_assert(kFwdThreads / 64 * 32 * ROWB <= 4 * TILEB, "acc staging");
+  const int share = wave * 32 * ROWB;
+  HCP_LDS(char)* const tbuf[4] = {K0, K1, V0, V1};
+  HCP_LDS(char)* const abuf = tbuf[share / TILEB] + share % TILEB;
+  if (p.acc_o != nullptr && wave_q0 < q_len) {
+    const int64_t sb = p.acc_stride_tok * 2;
+    const int rows = q_len - wave_q0 < 32 ? static_cast<int>(q_len - wave_q0) : 32;
+    const char* abase = reinterpret_cast<const char*>(p.acc_o) +
+                        ((e.q_start + wave_q0) * p.acc_stride_tok +
+                         static_cast<int64_t>(head) * p.acc_stride_head) * 2;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(abase), 0, static_cast<int>((rows - 1) * sb) + ROWB, kBufferRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < 32 / RPL; ++i) {
+      const int r = i * RPL + lane / CPR;
+      const int lc = (lane % CPR) ^ (r & (CPR - 1));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, reinterpret_cast<HCP_LDS(void)*>(abuf + i * 1024), 16,
+          static_cast<int>(r * sb) + lc * 16, 0, 0, 0);
+    }
+  }
   if (q_valid) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const int64_t row = e.q_start + qi;
     char* orow = reinterpret_cast<char*>(p.out) +
                  (row * p.o_stride_tok + static_cast<int64_t>(head) * p.o_stride_head) * 2;
+    float lse_row = l_tot > 0.f ? m_ref * kLn2 + __logf(l_tot) : -INFINITY;
+    if (p.acc_o == nullptr) {
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
+      for (int db = 0; db < DBLK; ++db) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d0 = 32 * db + 8 * a + 4 * g;
-        u32x2 w;
-        w[0] = pack2<T>(oacc[db][4 * a + 0] * inv, oacc[db][4 * a + 1] * inv);
-        w[1] = pack2<T>(oacc[db][4 * a + 2] * inv, oacc[db][4 * a + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * db + 8 * a + 4 * g;
+          u32x2 w;
+          w[0] = pack2<T>(oacc[db][4 * a + 0] * inv, oacc[db][4 * a + 1] * inv);
+          w[1] = pack2<T>(oacc[db][4 * a + 2] * inv, oacc[db][4 * a + 3] * inv);
+          *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
+        }
+      }
+    } else {
+      // LSE merge with the partial state acc, in merge_kernel's arithmetic:
+      // this pass's output enters as stored in the output dtype, a side of
+      // weight 0 enters as 0 (acc is then not read), out = fma(prefix, wp,
+      // suffix * ws), lse = m + log(e^{lp-m} + e^{ls-m}); an acc LSE of +inf
+      // counts as -inf.  The result equals this pass followed by
+      // merge_attn_states bit for bit.
+      float la = p.acc_lse[static_cast<int64_t>(head) * p.acc_lse_stride_head + row];
+      if (la == INFINITY) la = -INFINITY;
+      const bool acc_pre = p.acc_prefix != 0;
+      const float lp = acc_pre ? la : lse_row, ls = acc_pre ? lse_row : la;
+      const float m = __builtin_fmaxf(lp, ls);
+      float ps = 0.f, ss = 0.f;
+      if (m == -INFINITY) {
+        lse_row = -INFINITY;
+      } else {
+        const float wp = __expf(lp - m), ws = __expf(ls - m);
+        const float se = wp + ws;
+        ps = wp / se;
+        ss = ws / se;
+        lse_row = m + __logf(se);
+      }
+      const float w_acc = acc_pre ? ps : ss, w_own = acc_pre ? ss : ps;
+      wait_vmcnt<0>();  // this wave's rows have landed in abuf
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const int d0 = 32 * db + 8 * a + 4 * g;
+          u32x2 own;
+          own[0] = pack2<T>(oacc[db][4 * a + 0] * inv, oacc[db][4 * a + 1] * inv);
+          own[1] = pack2<T>(oacc[db][4 * a + 2] * inv, oacc[db][4 * a + 3] * inv);
+          if (!(w_own > 0.f)) own = u32x2{0, 0};
+          const u32x2 oth =
+              w_acc > 0.f ? *reinterpret_cast<const HCP_LDS(u32x2)*>(
+                                abuf + r32 * ROWB + (((4 * db + a) ^ (r32 & (CPR - 1))) * 16) + 8 * g)
+                          : u32x2{0, 0};
+          const u32x2 pre = acc_pre ? oth : own, suf = acc_pre ? own : oth;
+          u32x2 w;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float a0 = E::to_float(static_cast<uint16_t>(pre[h] & 0xffffu));
+            const float a1 = E::to_float(static_cast<uint16_t>(pre[h] >> 16));
+            const float b0 = E::to_float(static_cast<uint16_t>(suf[h] & 0xffffu));
+            const float b1 = E::to_float(static_cast<uint16_t>(suf[h] >> 16));
+            w[h] = pack2<T>(__builtin_fmaf(a0, ps, b0 * ss), __builtin_fmaf(a1, ps, b1 * ss));
+          }
+          *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
+        }
       }
     }
-    if (g == 0) {
-      p.lse[static_cast<int64_t>(head) * p.lse_stride_head + row] =
-          l_tot > 0.f ? m_ref * kLn2 + __logf(l_tot) : -INFINITY;
-    }
+    if (g == 0 && p.lse != nullptr) p.lse[static_cast<int64_t>(head) * p.lse_stride_head + row] = lse_row;
   }
 }
 

@@ -170,4 +170,12 @@ __device__ __forceinline__ bool xcd_remap(int64_t b, int64_t per_kvh,
   return *item < per_kvh;
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt
+// and lgkmcnt left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace hcp

@@ -38,13 +38,6 @@ constexpr int kBufWord3 = 0x00020000;
 constexpr int kStreamAux = 2;
 #define HCP_LDS_PTR(T) __attribute__((address_space(3))) T*
 
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt
-// and lgkmcnt left at "no wait")
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // LDS of the split kernel, shared by its paged and contiguous instantiations.
 template <int D>

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeParams p) {
                 (tok * p.s_stride_tok + head * p.s_stride_head + ch * 8) * dsize(p.s_dtype),
             p.s_dtype, b);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = a[i] * ps + b[i] * ss;
+    for (int i = 0; i < 8; ++i) out[i] = __builtin_fmaf(a[i], ps, b[i] * ss);
     lse_out = m + __logf(se);
   }
   store8(static_cast<char*>(p.out) +

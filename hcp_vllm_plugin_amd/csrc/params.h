@@ -27,6 +27,14 @@ struct FwdParams {
   float scale_log2;
   int32_t window;           // causal only: key j visible iff j > qpos - window (0: none)
   hcp_varlen_entry single;  // non-varlen: the one entry
+  // Optional partial state merged into the result (acc_o NULL: none).  Its
+  // rows are indexed like out's; acc_prefix says which side of the merge it
+  // is (1: prefix, this pass the suffix).  lse may then be NULL.
+  const void* acc_o;
+  int64_t acc_stride_tok, acc_stride_head;
+  const float* acc_lse;
+  int64_t acc_lse_stride_head;
+  int32_t acc_prefix;
 };
 
 struct DecParams {

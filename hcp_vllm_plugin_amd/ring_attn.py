@@ -6,6 +6,9 @@ shapes (q ``[Tq, H, D]``, k/v ``[Tk, Hkv, D]``, out ``[Tq, H, D]`` in q.dtype,
 lse ``[H, Tq]`` float32 natural log), ``causal_offset=None`` meaning
 non-causal and an integer meaning causal with query 0 at that position in the
 KV frame.  The work runs in ``hcp_attn_fwd_lse`` (libhcp_mi355x.so).
+
+``ring_attn_merged`` is that pass and the ``merge_attn_states`` after it
+(ring_backend.py:820-831) in one launch (``hcp_attn_fwd_lse_merge``).
 """
 
 from __future__ import annotations
@@ -14,7 +17,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["ring_attn_with_lse", "check_qkv"]
+__all__ = ["ring_attn_with_lse", "ring_attn_merged", "check_qkv"]
 
 
 def check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -90,3 +93,78 @@ def ring_attn_with_lse(
         )
     _lib.check(rc, "hcp_attn_fwd_lse")
     return out, lse
+
+
+def _check_partial(o: torch.Tensor, lse: torch.Tensor, q: torch.Tensor, name: str) -> None:
+    if o.shape != q.shape or o.dtype != q.dtype or o.device != q.device:
+        raise ValueError(f"{name} output must match q: {tuple(o.shape)} {o.dtype}")
+    if lse.shape != (q.shape[1], q.shape[0]) or lse.dtype != torch.float32 or lse.device != q.device:
+        raise ValueError(f"{name} lse must be float32 [H, Tq]")
+    if lse.stride(1) != 1:
+        raise ValueError(f"{name} lse must be contiguous along tokens")
+    if o.stride(-1) != 1 or o.data_ptr() % 16 or any(st % 8 for st in o.stride()[:-1]):
+        raise ValueError(f"{name} output layout not loadable (16-byte rows, head_dim contiguous)")
+
+
+def ring_attn_merged(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    causal_offset: int | None,
+    acc_output: torch.Tensor,
+    acc_lse: torch.Tensor,
+    acc_is_prefix: bool = True,
+    window: int | None = None,
+    output: torch.Tensor | None = None,
+    output_lse: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``ring_attn_with_lse`` over (q, k, v) merged with a partial state, in one launch.
+
+    With ``acc_is_prefix`` the result is ``merge_attn_states(output,
+    acc_output, acc_lse, <this pass>)`` -- the local pass taking the peer
+    result as the prefix, as ``HcpRingAttentionImpl.forward`` merges them
+    (ring_backend.py:349-354,820-831); otherwise this pass is the prefix.
+    The arithmetic is the merge kernel's on this pass's output rounded to
+    q.dtype, so the result equals the two calls bit for bit.  ``output``
+    (default: new) may be ``acc_output`` itself; ``output_lse`` (optional,
+    ``[H, Tq]`` float32) receives the merged LSE.  Returns ``output``.
+    """
+    check_qkv(q, k, v)
+    if window is not None and window <= 0:
+        raise ValueError("window must be a positive number of keys")
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    _check_partial(acc_output, acc_lse, q, "acc")
+    tq, num_heads, head_dim = q.shape
+    tk, num_kv_heads = k.shape[0], k.shape[1]
+    if output is None:
+        output = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif output.shape != q.shape or output.dtype != q.dtype or output.stride(-1) != 1:
+        raise ValueError("output must match q in shape and dtype, head_dim contiguous")
+    if output_lse is not None and (output_lse.shape != (num_heads, tq)
+                                   or output_lse.dtype != torch.float32
+                                   or output_lse.stride(1) != 1):
+        raise ValueError("output_lse must be float32 [H, Tq], contiguous along tokens")
+    if tq == 0:
+        return output
+    if k.stride() != v.stride():
+        v = v.contiguous()
+        k = k.contiguous()
+    L = _lib.lib()
+    with torch.cuda.device(q.device):
+        rc = L.hcp_attn_fwd_lse_merge(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(),
+            0 if output_lse is None else output_lse.data_ptr(),
+            tq, tk, num_heads, num_kv_heads, head_dim,
+            q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+            v.stride(0), v.stride(1), output.stride(0), output.stride(1),
+            0 if output_lse is None else output_lse.stride(0),
+            float(scale), 0 if causal_offset is None else 1,
+            0 if causal_offset is None else int(causal_offset),
+            0 if (window is None or causal_offset is None) else int(window),
+            acc_output.data_ptr(), acc_output.stride(0), acc_output.stride(1),
+            acc_lse.data_ptr(), acc_lse.stride(0), int(bool(acc_is_prefix)),
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
+        )
+    _lib.check(rc, "hcp_attn_fwd_lse_merge")
+    return output

@@ -15,9 +15,10 @@ Drop-in for hcp_vllm_plugin/ring_backend.py's hot path:
   and for the rest local causal attention over ``[peer_end, tk)`` at offset
   ``qpos0 + n_a - peer_end`` merged with non-causal attention over the peer.
   Instead of a Python loop with a gather copy and 5-6 launches per request,
-  a whole batch runs as one varlen launch over the paged cache (read in
-  place), one launch over the staged peer KV and one merge; a pure decode
-  batch runs the split-KV decode kernel.
+  a whole batch runs as one launch over the staged peer KV and one varlen
+  launch over the paged cache (read in place) that also merges the peer
+  result into the output; a pure decode batch runs the split-KV decode
+  kernel.
 * ``_attn`` / ``_merge`` (ring_backend.py:309-360) with ``HCP_RING_IMPL`` /
   ``HCP_RING_MERGE`` read on every call.  ``hip`` is the default; ``triton``
   is accepted as an alias so existing launch scripts keep working.  There is
@@ -35,7 +36,8 @@ Drop-in for hcp_vllm_plugin/ring_backend.py's hot path:
   decode batch the owner partials run in the same split-KV launch as the
   other rows.
 * ``IMPL_STATS`` evidence counters (ring_backend.py:295-306).  ``attn_hip`` /
-  ``merge_hip`` count kernel launches; the legacy keys ``attn_triton`` /
+  ``merge_hip`` count kernel launches and merges (a merge done inside the
+  local pass counts as one); the legacy keys ``attn_triton`` /
   ``merge_triton`` mirror them so validators that read those names still see
   which path ran, and ``attn_torch`` / ``merge_torch`` stay 0.
 """
@@ -716,15 +718,11 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
                                                          self.scale, self.sliding_window)
             _count("attn")
             return
-        o_loc = torch.empty_like(query, memory_format=torch.contiguous_format)
-        lse_loc = torch.full((h, query.shape[0]), float("-inf"), dtype=torch.float32, device=dev)
-        VarlenLaunch(plan.local, True, True, dev).run(query, o_loc, lse_loc, self.num_kv_heads,
-                                                     self.scale, self.sliding_window)
-        _count("attn")
         o_peer = lse_peer = None
         for rnd in plan.peer_rounds:
             o_r = torch.empty_like(query, memory_format=torch.contiguous_format)
-            lse_r = torch.full_like(lse_loc, float("-inf"))
+            lse_r = torch.full((h, query.shape[0]), float("-inf"), dtype=torch.float32,
+                               device=dev)
             for kind in ("contig", "paged"):
                 if rnd[kind]:
                     VarlenLaunch(rnd[kind], False, kind == "paged", dev).run(
@@ -738,8 +736,15 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
                 merge_attn_states(o_m, o_peer, lse_peer, o_r, lse_r, lse_m)
                 _count("merge")
                 o_peer, lse_peer = o_m, lse_m
-        # prefix = peer, suffix = local (ring_backend.py:354)
-        merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc)
+        # Local causal pass merged with the peer result in the same launch:
+        # merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc) with prefix
+        # = peer, suffix = local (ring_backend.py:354,820-831), bit for bit.
+        # The local entries cover every query row of the plan; rows without a
+        # peer have lse_peer = -inf and get the local result.
+        VarlenLaunch(plan.local, True, True, dev).run(
+            query, out, None, self.num_kv_heads, self.scale, self.sliding_window,
+            acc=(o_peer, lse_peer), acc_is_prefix=True)
+        _count("attn")
         _count("merge")
 
     def _forward_decode(self, query, out, plan: _Plan, n: int, ring_local=None):

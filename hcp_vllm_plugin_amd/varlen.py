@@ -326,28 +326,54 @@ class VarlenLaunch:
         self._plan_dev, (self.entries_ptr, self.tiles_ptr) = _upload([arr, tiles], device)
         self.device = device
 
-    def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
-            num_kv_heads: int, scale: float, window: int | None = None) -> None:
+    def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
+            num_kv_heads: int, scale: float, window: int | None = None,
+            acc=None, acc_is_prefix: bool = True) -> None:
         """``window``: sliding window of a causal launch (query at p sees keys
-        p - window < j <= p in its entry's frame); ignored when non-causal."""
+        p - window < j <= p in its entry's frame); ignored when non-causal.
+
+        ``acc=(o, lse)``: a partial state with out's rows, merged into the
+        result in the same launch (``hcp_attn_fwd_varlen_merge``): with
+        ``acc_is_prefix`` each row gets merge_attn_states(acc, this pass), the
+        local pass taking the peer result as the prefix (ring_backend.py:354).
+        ``lse`` may then be None; otherwise it receives the merged LSE."""
         if self.num_tiles == 0:
             return
         if window is not None and window <= 0:
             raise ValueError("window must be a positive number of keys")
         num_heads, head_dim = q.shape[1], q.shape[2]
         L = _lib.lib()
+        win = int(window or 0) if self.causal else 0
         with torch.cuda.device(q.device):
-            rc = L.hcp_attn_fwd_varlen(
+            if acc is None:
+                rc = L.hcp_attn_fwd_varlen(
+                    q.data_ptr(), q.stride(0), q.stride(1),
+                    out.data_ptr(), out.stride(0), out.stride(1),
+                    lse.data_ptr(), lse.stride(0),
+                    self.entries_ptr, self.num_entries,
+                    self.tiles_ptr, self.num_tiles,
+                    num_heads, num_kv_heads, head_dim, float(scale),
+                    int(self.causal), win, int(self.paged),
+                    _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
+                )
+                _lib.check(rc, "hcp_attn_fwd_varlen")
+                return
+            a_o, a_lse = acc
+            if a_o.dtype != q.dtype or a_o.stride(-1) != 1 or a_lse.dtype != torch.float32:
+                raise ValueError("acc must be (out in q.dtype, float32 lse)")
+            rc = L.hcp_attn_fwd_varlen_merge(
                 q.data_ptr(), q.stride(0), q.stride(1),
                 out.data_ptr(), out.stride(0), out.stride(1),
-                lse.data_ptr(), lse.stride(0),
+                0 if lse is None else lse.data_ptr(), 0 if lse is None else lse.stride(0),
                 self.entries_ptr, self.num_entries,
                 self.tiles_ptr, self.num_tiles,
                 num_heads, num_kv_heads, head_dim, float(scale),
-                int(self.causal), int(window or 0) if self.causal else 0, int(self.paged),
+                int(self.causal), win, int(self.paged),
+                a_o.data_ptr(), a_o.stride(0), a_o.stride(1),
+                a_lse.data_ptr(), a_lse.stride(0), int(bool(acc_is_prefix)),
                 _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device),
             )
-        _lib.check(rc, "hcp_attn_fwd_varlen")
+        _lib.check(rc, "hcp_attn_fwd_varlen_merge")
 
 
 def varlen_attn_with_lse(

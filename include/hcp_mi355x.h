@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 6
+#define HCP_ABI_VERSION 7
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -137,6 +137,36 @@ int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
                      void* stream);
 
 /*
+ * hcp_attn_fwd_lse with the LSE merge of its result and a partial state
+ * (acc_out [tq, H, D] in `dtype`, acc_lse [H, tq] f32) done in the same
+ * launch: out = merge(prefix, suffix), where the prefix is acc and the
+ * suffix this pass if acc_is_prefix != 0, the other way round otherwise;
+ * lse (may be NULL) receives the merged LSE.  Replaces one attention pass
+ * plus the merge that follows it in HcpRingAttentionImpl.forward -- the
+ * local pass with the peer result as the prefix, merge_attn_states(out,
+ * o_peer, lse_peer, o_loc, lse_loc) (ring_backend.py:820-831,349-354) -- so
+ * the pass's own output never goes through HBM.  The arithmetic is
+ * hcp_merge_attn_states' on this pass's output rounded to `dtype`: the
+ * result equals hcp_attn_fwd_lse followed by hcp_merge_attn_states bit for
+ * bit.  An acc LSE of +inf counts as -inf; a side of weight 0 is not read.
+ * out may alias acc_out and lse acc_lse (rows are read before they are
+ * written, by the same thread).
+ */
+int hcp_attn_fwd_lse_merge(const void* q, const void* k, const void* v, void* out,
+                           float* lse, int64_t tq, int64_t tk, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim,
+                           int64_t q_stride_tok, int64_t q_stride_head,
+                           int64_t k_stride_tok, int64_t k_stride_head,
+                           int64_t v_stride_tok, int64_t v_stride_head,
+                           int64_t o_stride_tok, int64_t o_stride_head,
+                           int64_t lse_stride_head, float scale, int32_t causal,
+                           int64_t causal_offset, int32_t window,
+                           const void* acc_out, int64_t acc_stride_tok,
+                           int64_t acc_stride_head, const float* acc_lse,
+                           int64_t acc_lse_stride_head, int32_t acc_is_prefix,
+                           int32_t dtype, void* stream);
+
+/*
  * Query-block size (rows per tile) used by the varlen prefill kernel for this
  * head_dim / dtype; tiles are (entry, q_block) pairs in these units.
  */
@@ -174,6 +204,28 @@ int hcp_attn_fwd_varlen(const void* q, int64_t q_stride_tok,
                         int32_t head_dim, float scale, int32_t causal,
                         int32_t window, int32_t paged, int32_t dtype,
                         void* stream);
+
+/*
+ * hcp_attn_fwd_varlen with the merge of hcp_attn_fwd_lse_merge: acc rows are
+ * indexed like out's (the entries' q rows).  Replaces the batch's local pass
+ * and final merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc) of
+ * HcpRingAttentionImpl.forward (ring_backend.py:820-831) in one launch; rows
+ * of the launch get merge(acc, this pass) exactly as the two-step path.
+ */
+int hcp_attn_fwd_varlen_merge(const void* q, int64_t q_stride_tok,
+                              int64_t q_stride_head, void* out,
+                              int64_t o_stride_tok, int64_t o_stride_head,
+                              float* lse, int64_t lse_stride_head,
+                              const hcp_varlen_entry* entries,
+                              int32_t num_entries, const int32_t* tiles,
+                              int32_t num_tiles, int32_t num_heads,
+                              int32_t num_kv_heads, int32_t head_dim,
+                              float scale, int32_t causal, int32_t window,
+                              int32_t paged, const void* acc_out,
+                              int64_t acc_stride_tok, int64_t acc_stride_head,
+                              const float* acc_lse, int64_t acc_lse_stride_head,
+                              int32_t acc_is_prefix, int32_t dtype,
+                              void* stream);
 
 /*
  * Host-side split planner for hcp_decode_splitkv.  Each entry is one query

@@ -211,6 +211,50 @@ def test_argument_validation_status_codes(L):
     assert rc == _lib.HCP_EUNSUPPORTED  # head_dim 12
 
 
+def _fwd_merge(L, **kw):
+    a = dict(q=16, k=16, v=16, out=16, lse=None, tq=4, tk=4, h=28, hkv=4, d=128, st=8,
+             causal=1, off=0, window=0, acc=16, acc_lse=16, acc_st=8, prefix=1,
+             dtype=_lib.DTYPE_BF16, scale=0.088)
+    a.update(kw)
+    s, h = a["st"], a["h"]
+    return L.hcp_attn_fwd_lse_merge(a["q"], a["k"], a["v"], a["out"], a["lse"], a["tq"], a["tk"],
+                                    h, a["hkv"], a["d"], s * h, s, s * a["hkv"], s,
+                                    s * a["hkv"], s, s * h, s, a["tq"], a["scale"], a["causal"],
+                                    a["off"], a["window"], a["acc"], a["acc_st"] * h,
+                                    a["acc_st"], a["acc_lse"], a["tq"], a["prefix"], a["dtype"],
+                                    None)
+
+
+def _varlen_merge(L, **kw):
+    a = dict(tiles=16, ntiles=1, acc=16, acc_lse=16, acc_st=8, lse=None)
+    a.update(kw)
+    return L.hcp_attn_fwd_varlen_merge(16, 8 * 28, 8, 16, 8 * 28, 8, a["lse"], 0, 16, 1,
+                                       a["tiles"], a["ntiles"], 28, 4, 128, 0.088, 1, 0, 1,
+                                       a["acc"], a["acc_st"] * 28, a["acc_st"], a["acc_lse"],
+                                       4, 1, _lib.DTYPE_BF16, None)
+
+
+def test_attn_merge_status_codes(L):
+    """Argument checks of the attention + merge entry points, all returned
+    before any launch; without a partial state the plain pass still needs lse."""
+    assert _fwd_merge(L, acc=None) == _lib.HCP_EINVAL
+    assert b"null merge partial" in L.hcp_last_error()
+    assert _fwd_merge(L, acc_lse=None) == _lib.HCP_EINVAL
+    assert _fwd_merge(L, acc=24) == _lib.HCP_EINVAL        # not 16-byte aligned
+    assert b"aligned" in L.hcp_last_error()
+    assert _fwd_merge(L, acc_st=12) == _lib.HCP_EINVAL     # stride not a multiple of 8
+    assert _fwd_merge(L, d=96) == _lib.HCP_EUNSUPPORTED
+    assert _fwd_merge(L, window=-1) == _lib.HCP_EINVAL
+    assert _fwd_merge(L, tq=0) == _lib.HCP_OK               # nothing to do, nothing launched
+    assert _fwd(L, lse=None) == _lib.HCP_EINVAL
+    assert b"hcp_attn_fwd_lse:" in L.hcp_last_error()
+    assert _varlen_merge(L, acc=None) == _lib.HCP_EINVAL
+    assert b"hcp_attn_fwd_varlen_merge" in L.hcp_last_error()
+    assert _varlen_merge(L, acc=40) == _lib.HCP_EINVAL
+    assert _varlen_merge(L, acc_st=4) == _lib.HCP_EINVAL
+    assert _varlen_merge(L, ntiles=0) == _lib.HCP_OK
+
+
 def _dec_acc(L, **kw):
     a = dict(q=16, acc_o=16, acc_lse=16, out=16, h=28, hkv=4, d=128, seqs=1, scale=0.1,
              dtype=_lib.DTYPE_BF16)
