@@ -725,7 +725,7 @@ def main():
             "local_causal_merged": {"ms": round(pre["local"]["ms"], 4),
                                     "tflops": round(loc_tf, 2),
                                     "frac": round(loc_tf / PEAK_BF16_TFLOPS, 4),
-                                    "traffic": traffic.get("fa_fwd_local", {}).get("bytes")},
+                                    "traffic": traffic.get("fa_fwd_local_merged", {}).get("bytes")},
             "peer": {"ms": round(pre["peer"]["ms"], 4), "tflops": round(peer_tf, 2),
                      "frac": round(peer_tf / PEAK_BF16_TFLOPS, 4)},
             "two_step": None if math.isnan(pre["merge"]["ms"]) else {
@@ -734,7 +734,6 @@ def main():
                          "merge_ms": round(pre["merge"]["ms"], 4),
                          "merge_gbs": round(pre["merge"]["bytes"] / (pre["merge"]["ms"] * 1e-3)
                                             / 1e9, 1),
-                         "merge_traffic": traffic.get("merge", {}).get("bytes"),
                          "step_ms": round(pre["local_plain"]["ms"] + pre["peer"]["ms"]
                                           + pre["merge"]["ms"], 4)},
         },
