@@ -37,9 +37,10 @@ import os
 import threading
 import time
 
-import safetensors.torch
 import torch
 
+from .packet import Packet, encode, replace
+from .packet import _NAMES as _DTYPE_NAMES
 from .peer_ingest import PeerIngest
 from .varlen import DecodeBatch, decode_attn, segment_contiguous
 
@@ -69,21 +70,13 @@ def growth_assignee(pos: int, ring_size: int, policy: str = "rr") -> int:
 # ---------------------------------------------------------------------------
 # Packet codec (the wire format)
 # ---------------------------------------------------------------------------
-def _bytes_tensor(s: str) -> torch.Tensor:
-    return torch.tensor(list(s.encode()), dtype=torch.uint8)
-
-
-def _tensor_str(t: torch.Tensor) -> str:
-    return bytes(t.tolist()).decode()
-
-
 class _HostStage:
     """One pinned host buffer, grown on demand, for the packet's tensors.
 
     ``down`` copies device tensors into it (asynchronously, on the current
     stream) and synchronises once; ``up`` stages host tensors into it and
-    issues asynchronous copies to the device, recording an event that the
-    next use of the buffer waits for.
+    issues one asynchronous copy of them all to the device, recording an
+    event that the next use of the buffer waits for.
     """
 
     def __init__(self):
@@ -111,6 +104,26 @@ class _HostStage:
         n = t.numel() * t.element_size()
         return buf[off:off + n].view(t.dtype).view(t.shape)
 
+    def up_bytes(self, fields: list, device) -> tuple[torch.Tensor, list[int]]:
+        """``fields``: uint8 arrays (e.g. a packet's byte ranges), staged with
+        numpy copies and sent up in one copy.  Returns the device buffer and
+        each field's byte offset in it."""
+        offs, o = [], 0
+        for f in fields:
+            o = (o + 255) & ~255
+            offs.append(o)
+            o += f.size
+        buf = self._get(o)
+        pin = buf.numpy()
+        for off, f in zip(offs, fields):
+            pin[off:off + f.size] = f
+        dev = torch.empty(max(o, 1), dtype=torch.uint8, device=device)
+        dev[:o].copy_(buf[:o], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(device))
+        self._busy = ev
+        return dev, offs
+
     def down(self, tensors: list[torch.Tensor]) -> list[torch.Tensor]:
         dev = [t for t in tensors if t.is_cuda]
         offs, total = self._layout(dev)
@@ -127,15 +140,16 @@ class _HostStage:
     def up(self, tensors: list[torch.Tensor], device) -> list[torch.Tensor]:
         offs, total = self._layout(tensors)
         buf = self._get(total)
-        out = []
         for off, t in zip(offs, tensors):
-            v = self._view(buf, off, t.contiguous())
-            v.copy_(t)
-            out.append(v.to(device, non_blocking=True))
+            self._view(buf, off, t).copy_(t)
+        # one host-to-device copy of the whole staging area into a fresh
+        # device buffer (so the returned tensors own their memory)
+        dev = torch.empty(max(total, 1), dtype=torch.uint8, device=device)
+        dev[:total].copy_(buf[:total], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(device))
         self._busy = ev
-        return out
+        return [self._view(dev, off, t) for off, t in zip(offs, tensors)]
 
 
 def encode_packet(q, o, lse, scale, layer, chunk, req="", growth_k=None, growth_v=None,
@@ -151,33 +165,26 @@ def encode_packet(q, o, lse, scale, layer, chunk, req="", growth_k=None, growth_
         ts += [growth_k.detach().contiguous(), growth_v.detach().contiguous()]
     if any(t.is_cuda for t in ts):
         ts = (stage or _HostStage()).down(ts)
-    d = {
-        "chunk": _bytes_tensor(chunk),
-        "layer": _bytes_tensor(layer),
-        "req": _bytes_tensor(req),
-        "q": ts[0],
-        "o": ts[1],
-        "lse": ts[2],
-        "scale": torch.tensor([float(scale)], dtype=torch.float32),
-    }
+    d = {"chunk": chunk, "layer": layer, "req": req, "q": ts[0], "o": ts[1], "lse": ts[2],
+         "scale": torch.tensor([float(scale)], dtype=torch.float32)}
     if with_growth:
         d["growth_k"], d["growth_v"] = ts[3], ts[4]
         d["growth_target"] = torch.tensor([int(growth_target)], dtype=torch.int64)
-    return safetensors.torch.save(d)
+    return encode(d)
 
 
 def decode_packet(payload: bytes) -> dict:
     """Parse a packet: strings decoded, ``scale`` / ``growth_target`` as
     Python numbers, tensors left on the host."""
-    t = safetensors.torch.load(payload)
-    out = dict(t)
+    pkt = Packet(payload)
+    out = {k: pkt.tensor(k) for k in pkt.meta}
     for k in ("chunk", "layer", "req"):
-        if k in t:
-            out[k] = _tensor_str(t[k])
+        if k in pkt:
+            out[k] = pkt.text(k)
     out.setdefault("req", "")
-    out["scale"] = float(t["scale"].item())
-    if "growth_target" in t:
-        out["growth_target"] = int(t["growth_target"].item())
+    out["scale"] = float(pkt.item("scale"))
+    if "growth_target" in pkt:
+        out["growth_target"] = int(pkt.item("growth_target"))
     return out
 
 
@@ -342,13 +349,7 @@ class RingDecodeNode:
         g.append(gk, gv)
         self._growth_appends[req] = self._growth_appends.get(req, 0) + 1
 
-    def accumulate(self, q: torch.Tensor, o_acc: torch.Tensor, lse_acc: torch.Tensor,
-                   scale: float, layer: str, req: str = "",
-                   chunk: str = "") -> tuple[torch.Tensor, torch.Tensor]:
-        """Device-only hop: (O, LSE) of the accumulator merged with this
-        node's partial over its chunk snapshot plus this request's growth
-        (non-causal), ring_decode.py:224-237.  The node's own chunk key is
-        used; ``chunk`` (the packet's) only when the node has none."""
+    def _accumulate_into(self, q, o_acc, lse_acc, scale, layer, req, chunk, out, lse) -> None:
         my_chunk = self._chunk_keys[0] if self._chunk_keys else chunk
         k, v = self._layers[(my_chunk, layer)]
         g = self._growth.get((req, layer))
@@ -360,47 +361,82 @@ class RingDecodeNode:
             plan = (sig, DecodeBatch([segs] * q.shape[0], q.shape[1], k.shape[1], q.shape[2],
                                      q.device))
             self._plans[(req, layer)] = plan
+        plan[1].run(q, out, lse, scale, acc=(o_acc, lse_acc))
+
+    def accumulate(self, q: torch.Tensor, o_acc: torch.Tensor, lse_acc: torch.Tensor,
+                   scale: float, layer: str, req: str = "",
+                   chunk: str = "") -> tuple[torch.Tensor, torch.Tensor]:
+        """Device-only hop: (O, LSE) of the accumulator merged with this
+        node's partial over its chunk snapshot plus this request's growth
+        (non-causal), ring_decode.py:224-237.  The node's own chunk key is
+        used; ``chunk`` (the packet's) only when the node has none."""
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
         lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32, device=q.device)
-        plan[1].run(q, out, lse, scale, acc=(o_acc, lse_acc))
+        self._accumulate_into(q, o_acc, lse_acc, scale, layer, req, chunk, out, lse)
         return out, lse
 
     def handle_packet(self, payload: bytes) -> bytes:
         """One hop on a packet (ring_decode.py:187-259): growth addressed to
         this node appended, partial merged into the accumulator, the updated
-        packet returned; growth for another node is forwarded unchanged."""
-        t = safetensors.torch.load(payload)
-        layer = _tensor_str(t["layer"])
-        req = _tensor_str(t["req"]) if "req" in t else ""
-        q_host = t["q"] if t["q"].dtype == self._dtype else t["q"].to(self._dtype)
-        o_host = t["o"] if t["o"].dtype == self._dtype else t["o"].to(self._dtype)
-        lse_host = t["lse"].to(torch.float32)
+        packet returned; growth for another node is forwarded unchanged.
+
+        Host side: the packet is parsed in place; q, o, lse (and consumed
+        growth) go up in one copy; the new O and LSE land in one device
+        buffer and come down in one copy; the reply is the received bytes with
+        the ``o`` and ``lse`` ranges rewritten whenever the key set and dtypes
+        stay the same (no re-serialisation)."""
+        pkt = Packet(payload)
+        layer = pkt.text("layer")
+        req = pkt.text("req") if "req" in pkt else ""
+        dname = _DTYPE_NAMES.get(self._dtype)
+        same = (pkt.meta["q"]["dtype"] == dname and pkt.meta["o"]["dtype"] == dname
+                and pkt.meta["lse"]["dtype"] == "F32")
         consumed = False
-        ups = [q_host, o_host, lse_host]
-        if "growth_k" in t:
-            target = (int(t["growth_target"].item()) if "growth_target" in t
-                      else self._ring_index)
+        if "growth_k" in pkt:
+            target = int(pkt.item("growth_target")) if "growth_target" in pkt else self._ring_index
             consumed = target == self._ring_index
-            if consumed:
-                ups += [t["growth_k"].to(self._dtype), t["growth_v"].to(self._dtype)]
-        dev = self._stage.up(ups, self._device)
+        names = ["q", "o", "lse"] + (["growth_k", "growth_v"] if consumed else [])
+        if same and (not consumed or (pkt.meta["growth_k"]["dtype"] == dname
+                                      and pkt.meta["growth_v"]["dtype"] == dname)):
+            # the packet's bytes go up as they are
+            buf, offs = self._stage.up_bytes([pkt.raw(n) for n in names], self._device)
+            dev = []
+            for n, off in zip(names, offs):
+                dt = torch.float32 if n == "lse" else self._dtype
+                nb = pkt.raw(n).size
+                dev.append(buf[off:off + nb].view(dt).view(pkt.shape(n)))
+        else:
+            dev = self._stage.up([pkt.tensor(n).to(torch.float32 if n == "lse" else self._dtype)
+                                  for n in names], self._device)
         q, o_acc, lse_acc = dev[0], dev[1], dev[2]
         if consumed:
             self.append_growth(req, layer, dev[3], dev[4])
-        o, lse = self.accumulate(q, o_acc, lse_acc, float(t["scale"].item()), layer, req,
-                                 _tensor_str(t["chunk"]))
+        # O and LSE in one device buffer, so they come down in one copy
+        no = q.numel() * q.element_size()
+        lo = (no + 255) & ~255
+        res = torch.empty(lo + q.shape[1] * q.shape[0] * 4, dtype=torch.uint8, device=q.device)
+        o = res[:no].view(q.dtype).view(q.shape)
+        lse = res[lo:].view(torch.float32).view(q.shape[1], q.shape[0])
+        self._accumulate_into(q, o_acc, lse_acc, float(pkt.item("scale")), layer, req,
+                              pkt.text("chunk"), o, lse)
         self._calls += 1
-        o_h, lse_h = self._stage.down([o, lse])
-        out = {"chunk": t["chunk"], "layer": t["layer"], "q": q_host, "o": o_h, "lse": lse_h,
-               "scale": t["scale"]}
-        if "req" in t:
-            out["req"] = t["req"]
-        if "growth_k" in t and not consumed:
-            out["growth_k"] = t["growth_k"]
-            out["growth_v"] = t["growth_v"]
-            if "growth_target" in t:
-                out["growth_target"] = t["growth_target"]
-        return safetensors.torch.save(out)
+        (res_h,) = self._stage.down([res])
+        if same and not consumed:
+            pin = res_h.numpy()
+            return replace(pkt, {"o": pin[:no], "lse": pin[lo:lo + q.shape[1] * q.shape[0] * 4]})
+        o_h = res_h[:no].view(q.dtype).view(q.shape)
+        lse_h = res_h[lo:].view(torch.float32).view(q.shape[1], q.shape[0])
+        out = {"chunk": pkt.tensor("chunk"), "layer": pkt.tensor("layer"),
+               "q": pkt.tensor("q").to(self._dtype), "o": o_h, "lse": lse_h,
+               "scale": pkt.tensor("scale")}
+        if "req" in pkt:
+            out["req"] = pkt.tensor("req")
+        if "growth_k" in pkt and not consumed:
+            out["growth_k"] = pkt.tensor("growth_k")
+            out["growth_v"] = pkt.tensor("growth_v")
+            if "growth_target" in pkt:
+                out["growth_target"] = pkt.tensor("growth_target")
+        return encode(out)
 
     # -- relay loop (non-owner nodes) ----------------------------------------
     def start_relay(self, transport) -> None:
@@ -450,8 +486,9 @@ def ring_decode_step(transport, q, o_acc, lse_acc, scale, layer, chunk, req="",
         stage = _OWNER_STAGE.stage = _HostStage()
     transport.send_packet(encode_packet(q, o_acc, lse_acc, scale, layer, chunk, req,
                                         growth_k, growth_v, growth_target, stage=stage))
-    t = safetensors.torch.load(transport.recv_packet(timeout_s=timeout_s))
+    pkt = Packet(transport.recv_packet(timeout_s=timeout_s))
+    o_h, lse_h = pkt.tensor("o").to(q.dtype), pkt.tensor("lse").to(torch.float32)
     if not q.is_cuda:
-        return t["o"].to(q.dtype), t["lse"].to(torch.float32)
-    o, lse = stage.up([t["o"].to(q.dtype), t["lse"].to(torch.float32)], q.device)
+        return o_h, lse_h
+    o, lse = stage.up([o_h, lse_h], q.device)
     return o, lse

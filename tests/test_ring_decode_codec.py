@@ -77,3 +77,65 @@ def test_growth_assignee():
     assert [growth_assignee(p, 3) for p in range(7)] == [0, 1, 2, 0, 1, 2, 0]
     assert [growth_assignee(p, 4, "rr") for p in (100, 101, 102, 103)] == [0, 1, 2, 3]
     assert all(growth_assignee(p, 5, "owner") == 4 for p in range(9))
+
+
+def test_in_place_reply_is_the_packet_with_o_and_lse_rewritten():
+    """The hop's reply (packet.replace): every field byte-identical except the
+    accumulator, and still a safetensors file plain safetensors reads."""
+    from hcp_vllm_plugin_amd.packet import Packet, replace
+
+    q, o, lse, gk, gv = _tensors()
+    pkt_bytes = encode_packet(q, o, lse, 0.25, "L3", "c1", "req9", gk, gv, 1)
+    pkt = Packet(pkt_bytes)
+    o2 = torch.randn(1, 28, 128).to(torch.bfloat16)
+    lse2 = torch.randn(28, 1)
+    out = replace(pkt, {"o": o2, "lse": lse2})
+    assert len(out) == len(pkt_bytes)
+    raw = safetensors.torch.load(out)
+    ref = safetensors.torch.load(pkt_bytes)
+    assert set(raw) == set(ref)
+    for k in ref:
+        if k not in ("o", "lse"):
+            assert torch.equal(raw[k], ref[k]), k
+    assert torch.equal(raw["o"], o2) and torch.equal(raw["lse"], lse2)
+    # only the two data ranges differ
+    diff = [i for i, (a, b) in enumerate(zip(out, pkt_bytes)) if a != b]
+    spans = [pkt.span("o"), pkt.span("lse")]
+    assert all(any(b <= i < e for b, e in spans) for i in diff)
+
+
+def test_packet_parser_details():
+    from hcp_vllm_plugin_amd.packet import Packet, encode, replace
+
+    q, o, lse, gk, gv = _tensors(torch.float16)
+    # a reference packet with metadata and an empty req reads through Packet
+    d = {"chunk": torch.tensor(list(b"c"), dtype=torch.uint8),
+         "req": torch.zeros(0, dtype=torch.uint8), "q": q, "lse": lse,
+         "scale": torch.tensor([0.5]), "growth_target": torch.tensor([7], dtype=torch.int64)}
+    pkt = Packet(safetensors.torch.save(d, metadata={"format": "pt"}))
+    assert pkt.text("chunk") == "c" and pkt.text("req") == ""
+    assert pkt.item("scale") == 0.5 and pkt.item("growth_target") == 7
+    assert torch.equal(pkt.tensor("q"), q) and torch.equal(pkt.tensor("lse"), lse)
+    # encode lays tensors out aligned to their element size, and strings as uint8
+    enc = encode({"req": "", "layer": "L", "q": q, "lse": lse,
+                  "t": torch.tensor([3], dtype=torch.int64)})
+    p2 = Packet(enc)
+    for name in p2.meta:
+        b, _ = p2.span(name)
+        assert b % p2.tensor(name).element_size() == 0, name
+    raw = safetensors.torch.load(enc)
+    assert bytes(raw["layer"].tolist()) == b"L" and raw["req"].numel() == 0
+    # malformed packets and mismatched replacements are rejected
+    for bad in (b"", b"\xff" * 8 + b"{}", enc[:20]):
+        try:
+            Packet(bad)
+        except ValueError:
+            pass
+        else:
+            raise AssertionError(f"accepted {bad[:12]!r}")
+    try:
+        replace(p2, {"q": q.to(torch.bfloat16)})
+    except ValueError:
+        pass
+    else:
+        raise AssertionError("dtype mismatch accepted")
