@@ -411,15 +411,28 @@ def bench_sliding_window(dev, steps, warmup, window=4096, n=8192):
     from hcp_vllm_plugin_amd import ring_attn_with_lse
 
     q, kl, vl, _, _ = prefill_inputs(dev)
-    ms = timed(lambda: ring_attn_with_lse(q, kl, vl, SCALE, 0, window), steps, warmup)
+    win = lambda: ring_attn_with_lse(q, kl, vl, SCALE, 0, window)
+    full = lambda: ring_attn_with_lse(q, kl, vl, SCALE, 0)
+    timed(full, 2, warmup)  # clocks settled before either is timed
+    ms = timed(win, steps, warmup)
+    ms_full = timed(full, steps, warmup)
     pairs = sum(min(i + 1, window) for i in range(n))
     flops = 4 * D * H * pairs
     tf = flops / (ms * 1e-3) / 1e12
+
+    def tile_wgs(w):  # (64-key tile x 128-row workgroup) units the kernel executes
+        return H * sum(-(-(qb * 128 + 128 - (0 if w is None else max(0, qb * 128 - w + 1)))
+                         // 64) for qb in range(n // 128))
+
     return {
         "workload": (f"local causal pass, {n} queries x {n} keys, sliding window {window}, "
-                     f"28/4 heads, head_dim 128, bf16"),
+                     f"28/4 heads, head_dim 128, bf16; the same pass without the window "
+                     f"timed right after"),
         "ms": round(ms, 4), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
         "tflop": round(flops / 1e12, 3),
+        "ns_per_tile": round(ms * 1e6 / tile_wgs(window), 2),
+        "no_window": {"ms": round(ms_full, 4),
+                      "ns_per_tile": round(ms_full * 1e6 / tile_wgs(None), 2)},
     }
 
 
