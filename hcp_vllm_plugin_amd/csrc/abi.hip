@@ -205,6 +205,12 @@ int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries, 
   for (int32_t i = 0; i < num_entries; ++i) {
     const hcp_varlen_entry& en = entries[i];
     if (en.q_len < 0 || en.kv.len < 0) return fail(HCP_EINVAL, "%s: entry %d negative", who, i);
+    // the prefill kernel reads a wave's 16 rows of a paged tile from one block
+    if (en.kv.block_table && (en.kv.stride_tok <= 0 || en.kv.stride_tok >= (int64_t{1} << 24)))
+      return fail(HCP_EUNSUPPORTED, "%s: entry %d: paged token stride must be in (0, 2^24)", who, i);
+    if (en.kv.block_table && en.kv.block_size < hcp::kFwdPagedMinBlock)
+      return fail(HCP_EUNSUPPORTED, "%s: entry %d: paged prefill needs block_size >= %d, got %d",
+                  who, i, hcp::kFwdPagedMinBlock, en.kv.block_size);
     const int64_t nqb = (en.q_len + block_m - 1) / block_m;
     for (int64_t b = 0; b < nqb; ++b) {
       int64_t keys = en.kv.len;

@@ -87,12 +87,6 @@ __device__ __forceinline__ int tile_swz(int row) {
   return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
 }
 
-__device__ __forceinline__ void lds_load16(const char* g, HCP_LDS(char)* l) {
-  __builtin_amdgcn_global_load_lds(
-      reinterpret_cast<const __attribute__((address_space(1))) void*>(reinterpret_cast<uintptr_t>(g)),
-      reinterpret_cast<HCP_LDS(void)*>(l), 16, 0, 0);
-}
-
 template <typename V8>
 __device__ __forceinline__ V8 lds_read16(const HCP_LDS(char)* p) {
   return __builtin_bit_cast(V8, *reinterpret_cast<const HCP_LDS(u32x4)*>(p));
@@ -163,6 +157,17 @@ fa_fwd_kernel(FwdParams p) {
       e.causal_offset -= lo;
     }
   }
+  // Paged segments are tiled from a 64-key boundary of the request's block
+  // frame: with block_size >= 16 each wave's rows of a tile then lie in one
+  // block.  The `lead` keys in front of the segment load as zeros and are
+  // masked for every row.
+  int lead = 0;
+  if constexpr (PAGED) {
+    lead = static_cast<int>(e.kv.start & (BN - 1));
+    e.kv.start -= lead;
+    e.kv.len += lead;
+    e.causal_offset += lead;
+  }
   const int64_t q_len = e.q_len;
   const int kv_len = static_cast<int>(e.kv.len);
   const int64_t off = e.causal_offset;
@@ -215,6 +220,7 @@ fa_fwd_kernel(FwdParams p) {
     return (((lane * 16) % ROWB) / 16) ^ tile_swz<D>(lrow(i));
   };
   const int64_t rowb_g = e.kv.stride_tok * 2;  // bytes between tokens in HBM
+  const uint32_t rowb32 = static_cast<uint32_t>(rowb_g);
   const char* kseg;
   const char* vseg;
   int bs_shift = 0, bs_mask = 0;
@@ -232,108 +238,79 @@ fa_fwd_kernel(FwdParams p) {
     vseg = reinterpret_cast<const char*>(e.kv.v_addr) + base;
   }
 
-  // Paged segments whose cache spans less than 4 GiB from this head's base
-  // are read with buffer loads over one descriptor for the whole cache: the
-  // per-lane 32-bit byte offset of a row replaces its block id, loads are
-  // spread under phase A like contiguous ones, and a block id past the cache
-  // reads zeros instead of faulting.  Larger caches use global loads.
-  bool pbuf = false;
-  __amdgpu_buffer_rsrc_t rs_pk, rs_pv;
-  if constexpr (PAGED) {
-    const uint64_t span = static_cast<uint64_t>(e.kv.num_blocks) * static_cast<uint64_t>(blockb);
-    pbuf = e.kv.num_blocks > 0 && span < (uint64_t{1} << 32) && e.kv.block_size <= BN;
-    const int nrec = pbuf ? static_cast<int>(static_cast<uint32_t>(span)) : 0;
-    rs_pk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kseg), 0, nrec, kBufferRsrcWord3);
-    rs_pv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vseg), 0, nrec, kBufferRsrcWord3);
-  }
-
-  // paged: block ids of the lane's rows.  Tile j's K is issued at iteration
-  // j-2 and its V at iteration j-1, so three tiles' ids are live: bid_v (tile
-  // n+1), bid_k (tile n+2) and bid_f (tile n+3, fetched during iteration n).
-  // With buffer loads, a tile's ids become byte offsets from the head's base
-  // at the start of the iteration that issues its K -- one iteration after
-  // the fetch, so the conversion never waits on the block-table load.
-  uint32_t bid_v[NI], bid_k[NI], bid_f[NI];
-  auto fetch_blocks = [&](int tile_idx, uint32_t (&dst)[NI]) __attribute__((always_inline)) {
-    if constexpr (PAGED) {
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        int key = tile_idx * BN + lrow(i);
-        key = key < kv_len ? key : kv_len - 1;
-        dst[i] = static_cast<uint32_t>(bt[(e.kv.start + key) >> bs_shift]);
-      }
-    }
-  };
-  auto to_offsets = [&](int tile_idx, uint32_t (&ids)[NI]) __attribute__((always_inline)) {
-    if constexpr (PAGED) {
-      // block_size <= BN: a row's offset inside its block does not depend on
-      // the tile, except on a ragged tile whose rows past the end are clamped
-      // to the last key (a valid row: unused cache slots may hold NaNs)
-      const bool ragged = tile_idx * BN + BN > kv_len;
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        int key = tile_idx * BN + lrow(i);
-        if (ragged) key = key < kv_len ? key : kv_len - 1;
-        const uint32_t x = static_cast<uint32_t>(e.kv.start + key);
-        ids[i] = ids[i] * static_cast<uint32_t>(blockb) +
-                 (x & static_cast<uint32_t>(bs_mask)) * static_cast<uint32_t>(rowb_g) +
-                 lchunk(i) * 16u;
-      }
-    }
-  };
-
-  // contiguous: per-lane 32-bit byte offsets inside a tile (loop invariant);
-  // the tile base is wave-uniform, so loads use the SGPR-base + VGPR-offset form
-  const uint32_t rowb32 = static_cast<uint32_t>(rowb_g);
+  // Per-lane 32-bit byte offsets (loop invariant) under a wave-uniform
+  // descriptor, the SGPR-base + VGPR-offset form of buffer_load ... lds:
+  // contiguous segments rebase a descriptor per tile and offset by the tile
+  // row; paged ones rebase it per tile at the wave's first row -- its WROWS
+  // rows lie in one block -- and offset by the row inside the wave's share.
+  constexpr int WROWS = NI * RPI;  // tile rows each wave loads
+  static_assert(!PAGED || WROWS <= kFwdPagedMinBlock, "a wave's rows must fit one block");
   uint32_t goff[NI];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) goff[i] = lrow(i) * rowb32 + lchunk(i) * 16u;
+  for (int i = 0; i < NI; ++i)
+    goff[i] = static_cast<uint32_t>(PAGED ? lrow(i) - wave * WROWS : lrow(i)) * rowb32 +
+              lchunk(i) * 16u;
 
-  // Issue the global->LDS loads of one tile of K or V.  Ragged tiles clamp
+  // paged: block id of the wave's rows of tile t (clamped to the last tile,
+  // and to the segment's last key, so the block-table read stays in the
+  // request's row).  A vector load: a scalar one would share lgkmcnt with the
+  // LDS operand reads and serialise their waits.
+  auto fetch_id = [&](int t) __attribute__((always_inline)) {
+    uint32_t id = 0;
+    if constexpr (PAGED) {
+      t = t < ntiles ? t : ntiles - 1;
+      int key = t * BN + wave * WROWS;
+      key = key < kv_len ? key : kv_len - 1;
+      int idx = static_cast<int>((e.kv.start + key) >> bs_shift);
+      asm volatile("" : "+v"(idx));
+      id = static_cast<uint32_t>(bt[idx]);
+    }
+    return id;
+  };
+  // paged: descriptor of the wave's rows of tile t (clamped to the last
+  // tile), based at its first row; num_records ends at the segment's last key
+  // and at the block's end, so nothing past either is read (those rows read
+  // as zeros: unused cache slots may hold NaNs).  A block id past the cache
+  // is clamped to its last block.
+  auto page_rsrc = [&](const char* seg, uint32_t id_v, int t) __attribute__((always_inline)) {
+    t = t < ntiles ? t : ntiles - 1;
+    uint32_t id = __builtin_amdgcn_readfirstlane(id_v);
+    if (e.kv.num_blocks > 0 && id >= static_cast<uint64_t>(e.kv.num_blocks))
+      id = static_cast<uint32_t>(e.kv.num_blocks - 1);
+    const int r0 = t * BN + wave * WROWS;
+    const int in_blk = static_cast<int>((e.kv.start + r0) & bs_mask);
+    int rows = kv_len - r0;
+    rows = rows < WROWS ? rows : WROWS;
+    rows = rows < e.kv.block_size - in_blk ? rows : e.kv.block_size - in_blk;
+    const int nrec = rows > 0 ? static_cast<int>((rows - 1) * rowb_g) + ROWB : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(seg + static_cast<int64_t>(id) * blockb + in_blk * rowb_g), 0, nrec,
+        kBufferRsrcWord3);
+  };
+
+  // Contiguous prologue loads of one tile of K or V.  Ragged tiles clamp
   // their key rows into the segment (those rows are masked in S, and their
   // finite V values meet P = 0), so no load leaves the segment.
-  auto issue = [&](const char* seg, int tile_idx, const uint32_t (&bids)[NI],
-                   HCP_LDS(char)* dst) __attribute__((always_inline)) {
+  auto issue = [&](const char* seg, int tile_idx, HCP_LDS(char)* dst) __attribute__((always_inline)) {
     const int n0 = tile_idx * BN;
     const bool ragged = n0 + BN > kv_len;
-    if constexpr (PAGED) {
-      if (pbuf) {
-        const __amdgpu_buffer_rsrc_t rs = seg == kseg ? rs_pk : rs_pv;
+    // MUBUF form (buffer_load ... lds) over a descriptor rebased per tile:
+    // 32-bit offsets never overflow, and unlike the FLAT-encoded
+    // global_load_lds it leaves the compiler exact LDS-read wait counts
+    const char* base = seg + static_cast<int64_t>(n0) * rowb_g;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(base), 0, 0x7fffffff, kBufferRsrcWord3);
 #pragma unroll
-        for (int i = 0; i < NI; ++i)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
-              static_cast<int>(bids[i]), 0, 0, 0);
-        return;
+    for (int i = 0; i < NI; ++i) {
+      uint32_t o = goff[i];
+      if (ragged) {
+        const int key = n0 + lrow(i);
+        const int kc = key < kv_len ? key : kv_len - 1;
+        o = static_cast<uint32_t>(kc - n0) * rowb32 + lchunk(i) * 16u;
       }
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        int key = n0 + lrow(i);
-        if (ragged) key = key < kv_len ? key : kv_len - 1;
-        const int64_t x = e.kv.start + key;
-        const int64_t go =
-            static_cast<int64_t>(bids[i]) * blockb + (x & bs_mask) * rowb_g + lchunk(i) * 16;
-        lds_load16(seg + go, dst + (wave * NI + i) * 1024);
-      }
-    } else {
-      // MUBUF form (buffer_load ... lds) over a descriptor rebased per tile:
-      // 32-bit offsets never overflow, and unlike the FLAT-encoded
-      // global_load_lds it leaves the compiler exact LDS-read wait counts
-      const char* base = seg + static_cast<int64_t>(n0) * rowb_g;
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<char*>(base), 0, 0x7fffffff, kBufferRsrcWord3);
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        uint32_t o = goff[i];
-        if (ragged) {
-          const int key = n0 + lrow(i);
-          const int kc = key < kv_len ? key : kv_len - 1;
-          o = static_cast<uint32_t>(kc - n0) * rowb32 + lchunk(i) * 16u;
-        }
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
-            static_cast<int>(o), 0, 0, 0);
-      }
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
+          static_cast<int>(o), 0, 0, 0);
     }
   };
 
@@ -351,19 +328,17 @@ fa_fwd_kernel(FwdParams p) {
         const_cast<char*>(seg + static_cast<int64_t>(t) * BN * rowb_g), 0, nrec,
         kBufferRsrcWord3);
   };
-  auto load_one = [&](__amdgpu_buffer_rsrc_t rs, int i, HCP_LDS(char)* dst)
-      __attribute__((always_inline)) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
-        static_cast<int>(goff[i]), 0, 0, 0);
-  };
-  // the same with the lane's offset given (paged rows)
   auto load_at = [&](__amdgpu_buffer_rsrc_t rs, uint32_t o, int i, HCP_LDS(char)* dst)
       __attribute__((always_inline)) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, reinterpret_cast<HCP_LDS(void)*>(dst + (wave * NI + i) * 1024), 16,
         static_cast<int>(o), 0, 0, 0);
   };
+  auto load_one = [&](__amdgpu_buffer_rsrc_t rs, int i, HCP_LDS(char)* dst)
+      __attribute__((always_inline)) { load_at(rs, goff[i], i, dst); };
+  // paged: block ids of the wave's rows of tiles n+1 (V), n+2 (K) and n+3
+  // (fetched during iteration n, used two iterations later)
+  uint32_t id_v = 0, id_k = 0, id_f = 0;
   // phase A issues one K or V load instruction every kLoadEvery/2 MFMAs
   constexpr int kLoadEvery = 4;
 
@@ -419,7 +394,7 @@ fa_fwd_kernel(FwdParams p) {
   auto needs_mask = [&](int n) __attribute__((always_inline)) {
     const int n0 = n * BN;
     return (n0 + BN > kv_len) || (CAUSAL && (n0 + BN - 1 > off + wave_q0)) ||
-           (win > 0 && n0 < off + wave_q0 + 32 - win);
+           (win > 0 && n0 < off + wave_q0 + 32 - win) || (PAGED && n0 < lead);
   };
   auto apply_mask = [&](f32x16 (&S)[2], int n) __attribute__((always_inline)) {
     const int n0 = n * BN;
@@ -427,8 +402,10 @@ fa_fwd_kernel(FwdParams p) {
     const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
     const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
     const int lim = lim_r < lim_c ? lim_r : lim_c;
-    // lowest visible key of the lane's row, relative to the tile
-    const int64_t lo64 = win > 0 ? off + qi - win + 1 - n0 : 0;
+    // lowest visible key of the lane's row, relative to the tile (the window's
+    // bound, and the paged alignment lead)
+    int64_t lo64 = win > 0 ? off + qi - win + 1 - n0 : 0;
+    if (PAGED && lead - n0 > lo64) lo64 = lead - n0;
     const int lo = lo64 > 0 ? (lo64 < BN ? static_cast<int>(lo64) : BN) : 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -572,9 +549,8 @@ fa_fwd_kernel(FwdParams p) {
   constexpr int NB = 4 * DBLK;    // MFMAs in phase B
   constexpr int EB = 32 / NB;     // scores summed / maxed per phase-B MFMA
   auto phase_a = [&](const HCP_LDS(char)* Ks, f32x16 (&Sc)[2], f32x16 (&Sn)[2],
-                     __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst, bool loads,
-                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2, bool loads2,
-                     const uint32_t (&ko)[NI], const uint32_t (&vo)[NI])
+                     __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst,
+                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2)
       __attribute__((always_inline)) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     constexpr int KR = HCP_KPF + 1;  // K fragment ring
@@ -596,17 +572,10 @@ fa_fwd_kernel(FwdParams p) {
       constexpr int LE = kLoadEvery / 2;
       if (st % LE == 0 && st / LE < 2 * NI) {
         const int i = st / LE;
-        if (i % 2 == 0) {
-          if (loads) {
-            if constexpr (PAGED) load_at(rs, ko[i / 2], i / 2, ldst);
-            else load_one(rs, i / 2, ldst);
-          }
-        } else {
-          if (loads2) {
-            if constexpr (PAGED) load_at(rs2, vo[i / 2], i / 2, ldst2);
-            else load_one(rs2, i / 2, ldst2);
-          }
-        }
+        if (i % 2 == 0)
+          load_one(rs, i / 2, ldst);
+        else
+          load_one(rs2, i / 2, ldst2);
       }
       // scores st*EA .. st*EA+EA-1 of the current tile
 #pragma unroll
@@ -665,56 +634,35 @@ fa_fwd_kernel(FwdParams p) {
   auto iterate = [&](int n, f32x16 (&Sc)[2], f32x16 (&Sn)[2], HCP_LDS(char)* kload,
                      HCP_LDS(char)* vload, const HCP_LDS(char)* Ks,
                      const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
-    // loads for the next iteration: K(n+2) -> kload, V(n+1) -> vload.
-    // Contiguous and buffer-paged tiles are issued one load at a time under
-    // the MFMAs of phase A; globally-paged tiles are issued here.
-    bool spread;
+    // loads for the next iteration: K(n+2) -> kload, V(n+1) -> vload, one
+    // load instruction at a time under the MFMAs of phase A (a wave that
+    // computes nothing this iteration issues them here).  Tiles past the
+    // segment are clamped to its last one: they fill a buffer nobody reads.
     __amdgpu_buffer_rsrc_t rsk, rsv;
-    bool lk = true, lv = true;  // K(n+2) / V(n+1) exist (paged) or are clamped (contiguous)
     if constexpr (PAGED) {
-      rsk = rs_pk;
-      rsv = rs_pv;
-      lk = n + 2 < ntiles;
-      lv = n + 1 < ntiles;
-      if (pbuf && lk) to_offsets(n + 2, bid_k);  // fetched one iteration ago
-      if (!pbuf) {
-        if (lk) issue(kseg, n + 2, bid_k, kload);
-        if (lv) issue(vseg, n + 1, bid_v, vload);
-      }
-      if (n + 3 < ntiles) fetch_blocks(n + 3, bid_f);
-      spread = pbuf && n < wtiles;
-      if (pbuf && !spread) {
-        if (lk) issue(kseg, n + 2, bid_k, kload);
-        if (lv) issue(vseg, n + 1, bid_v, vload);
-      }
+      rsk = page_rsrc(kseg, id_k, n + 2);  // id fetched two iterations ago
+      rsv = page_rsrc(vseg, id_v, n + 1);
+      id_f = fetch_id(n + 3);
     } else {
       rsk = tile_rsrc(kseg, n + 2);
       rsv = tile_rsrc(vseg, n + 1);
-      spread = n < wtiles;
-      if (!spread) {
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          load_one(rsk, i, kload);
-          load_one(rsv, i, vload);
-        }
-      }
     }
     if (n < wtiles) {
-      if constexpr (PAGED)
-        phase_a(Ks, Sc, Sn, rsk, kload, spread && lk, rsv, vload, spread && lv, bid_k, bid_v);
-      else
-        phase_a(Ks, Sc, Sn, rsk, kload, spread, rsv, vload, spread, goff, goff);
+      phase_a(Ks, Sc, Sn, rsk, kload, rsv, vload);
       if (needs_mask(n + 1)) apply_mask(Sn, n + 1);
       float mh;
       phase_b(Vs, Sc, Sn, mh);
       if (n + 1 < wtiles) check_rescale(mh);
-    }
-    if constexpr (PAGED) {
+    } else {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        bid_v[i] = bid_k[i];
-        bid_k[i] = bid_f[i];
+        load_one(rsk, i, kload);
+        load_one(rsv, i, vload);
       }
+    }
+    if constexpr (PAGED) {
+      id_v = id_k;
+      id_k = id_f;
     }
     __syncthreads();  // waits for this iteration's tile loads (vmcnt(0)) first
   };
@@ -726,16 +674,29 @@ fa_fwd_kernel(FwdParams p) {
 
   // ---- prologue: K(0), K(1), V(0) in flight; S(0) = K(0) Q^T ----
   if (ntiles > 0) {
-    fetch_blocks(0, bid_f);
-    if (pbuf) to_offsets(0, bid_f);
-    issue(kseg, 0, bid_f, K0);
-    issue(vseg, 0, bid_f, V0);
-    if (ntiles > 1) {
-      fetch_blocks(1, bid_v);
-      if (pbuf) to_offsets(1, bid_v);
-      issue(kseg, 1, bid_v, K1);
+    if constexpr (PAGED) {
+      const uint32_t id0 = fetch_id(0);
+      id_v = fetch_id(1);  // V(1), issued in iteration 0
+      id_k = fetch_id(2);  // K(2), issued in iteration 0
+      // tile 0: the alignment lead's rows read as zeros (an offset past any
+      // num_records), whatever the cache holds there
+      const __amdgpu_buffer_rsrc_t rk0 = page_rsrc(kseg, id0, 0), rv0 = page_rsrc(vseg, id0, 0);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const uint32_t o = lrow(i) < lead ? 0x80000000u : goff[i];
+        load_at(rk0, o, i, K0);
+        load_at(rv0, o, i, V0);
+      }
+      if (ntiles > 1) {
+        const __amdgpu_buffer_rsrc_t rk1 = page_rsrc(kseg, id_v, 1);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) load_one(rk1, i, K1);
+      }
+    } else {
+      issue(kseg, 0, K0);
+      issue(vseg, 0, V0);
+      if (ntiles > 1) issue(kseg, 1, K1);
     }
-    if (ntiles > 2) fetch_blocks(2, bid_k);
   }
   __syncthreads();
   if (wtiles > 0) {

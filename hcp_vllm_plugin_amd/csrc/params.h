@@ -12,6 +12,7 @@ namespace hcp {
 constexpr int kFwdThreads = 64 * HCP_FWD_WAVES;
 constexpr int kFwdBM = 32 * HCP_FWD_WAVES;  // query rows per prefill workgroup
 constexpr int kFwdBN = 64;                  // keys per prefill tile
+constexpr int kFwdPagedMinBlock = 16;      // paged prefill: rows a wave reads from one block
 
 struct FwdParams {
   const void* q;

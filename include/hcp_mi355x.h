@@ -177,7 +177,9 @@ int hcp_varlen_block_m(int32_t head_dim, int32_t dtype);
  * entries, writes up to `cap` (entry, q_block) int32 pairs into host memory
  * `tiles_out`, heaviest tile first (longest-processing-time order), and
  * returns the number of tiles (or a negative status; HCP_EWORKSPACE if cap is
- * too small).  Runs on the CPU only.
+ * too small; HCP_EUNSUPPORTED for a paged entry with block_size < 16, since the
+ * prefill kernel reads each 16-row share of a 64-key tile from one block).
+ * Runs on the CPU only.
  */
 int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries,
                           int32_t causal, int32_t block_m, int32_t* tiles_out,

@@ -110,6 +110,22 @@ def test_plan_varlen_tiles_covers_every_block_longest_first(L, causal):
     assert b"need" in L.hcp_last_error()
 
 
+def test_plan_varlen_tiles_rejects_small_paged_blocks(L):
+    """Paged prefill reads each wave's 16 rows of a tile from one block."""
+    arr = (VarlenEntry * 2)(_entry(0, 100, 0, 300), _entry(100, 50, 0, 200))
+    for bs, want in ((8, _lib.HCP_EUNSUPPORTED), (16, None), (32, None)):
+        arr[1].kv.block_table = 0x2000
+        arr[1].kv.block_size = bs
+        arr[1].kv.stride_block = 4 * bs * 256
+        tiles = (ctypes.c_int32 * 64)()
+        rc = L.hcp_plan_varlen_tiles(arr, 2, 1, 128, tiles, 32)
+        if want is None:
+            assert rc > 0, (bs, rc)
+        else:
+            assert rc == want, (bs, rc)
+            assert b"block_size >= 16" in L.hcp_last_error()
+
+
 def test_plan_decode_splits_partition_each_segment(L):
     # 3 sequences: (kv lens of its entries)
     seqs = [[4096, 700], [0, 1], [33, 2048, 5]]

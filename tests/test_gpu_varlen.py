@@ -108,3 +108,58 @@ def test_varlen_offsets_and_unaligned_starts(dev):
         assert max_err(o_[qs:qs + L], ro) <= OUT_TOL[torch.bfloat16]
         assert max_err(lse_[:, qs:qs + L], rl) <= LSE_TOL
         qs += L
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_paged_cache_past_4gib_nan_outside_segments(dev, causal):
+    """Blocks at byte offsets past 4 GiB, segment starts off the 64-key tile
+    grid (the kernel aligns tiles down and zero-loads the lead), ragged ends;
+    every cache slot outside the segments holds NaN, so reading any of them
+    would show in the result."""
+    h, hkv, d, bs = 28, 4, 128, 16
+    blk_bytes = hkv * bs * 2 * d * 2
+    nb = 4_600_000_000 // blk_bytes + 1  # 4.6 GB [nb, 4, 16, 256] bf16 cache
+    cache = torch.full((nb, hkv, bs, 2 * d), float("nan"), dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator().manual_seed(77)
+    reqs = [(37, 300), (0, 129), (64, 1), (15, 700), (100, 33)]  # (segment start, length)
+    rows, qs_list, ks, vs = [], [], [], []
+    next_hi = nb - 1  # allocate blocks downward from the top of the cache
+    for start, ln in reqs:
+        nblk = -(-(start + ln) // bs)
+        ids = list(range(next_hi - nblk + 1, next_hi + 1))[::-1]
+        next_hi -= nblk
+        rows.append(ids)
+        k = randn(gen, (ln, hkv, d), torch.bfloat16)
+        v = randn(gen, (ln, hkv, d), torch.bfloat16)
+        for j in range(ln):  # only the segment's slots get data
+            pos = start + j
+            cache[ids[pos // bs], :, pos % bs, :d] = k[j].to(dev)
+            cache[ids[pos // bs], :, pos % bs, d:] = v[j].to(dev)
+        ks.append(k)
+        vs.append(v)
+    assert min(min(r) for r in rows) * blk_bytes > (1 << 32)
+    maxb = max(len(r) for r in rows)
+    bt = torch.zeros(len(reqs), maxb, dtype=torch.int32)
+    for r, ids in enumerate(rows):
+        bt[r, :len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    btd = bt.to(dev)
+    pc = PagedCache.from_tensor(cache)
+    q = randn(gen, (sum(ln for _, ln in reqs), h, d), torch.bfloat16)
+    qd = q.to(dev)
+    ents, qs = [], 0
+    for r, (start, ln) in enumerate(reqs):
+        ents.append(make_entry(qs, ln, segment_paged(pc, btd[r], start, ln), 0))
+        qs += ln
+    scale = scale_for(d)
+    out, lse = varlen_attn_with_lse(qd, ents, causal, hkv, scale)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any() and not torch.isnan(lse).any()
+    qs = 0
+    for r, (start, ln) in enumerate(reqs):
+        ro, rl = orc.attn_with_lse(q[qs:qs + ln].float(), ks[r].float(), vs[r].float(), scale,
+                                   0 if causal else None)
+        sl = slice(qs, qs + ln)
+        assert max_err(out[sl], ro) <= OUT_TOL[torch.bfloat16], r
+        assert max_err(lse[:, sl], rl) <= LSE_TOL, r
+        qs += ln
+    del cache
