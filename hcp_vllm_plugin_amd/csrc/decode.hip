@@ -232,7 +232,7 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
   // the cache spans less than 4 GiB from this head's base the DMA is a
   // bounds-checked buffer load over one descriptor for the whole cache (a
   // block id past the cache reads zeros); otherwise a global load with a
-  // 64-bit address.
+  // 64-bit address (a block id past the cache clamped to its last block).
   if constexpr (PAGED) {
     const int64_t blockb = kva.stride_block * 2;
     const uint64_t span = static_cast<uint64_t>(e.kv.num_blocks) * static_cast<uint64_t>(blockb);
@@ -253,6 +253,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
           __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kva.k + hb), 0, nrec, kBufWord3);
       const __amdgpu_buffer_rsrc_t rv =
           __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(kva.v + hb), 0, nrec, kBufWord3);
+      const uint32_t id_max = __builtin_amdgcn_readfirstlane(
+          e.kv.num_blocks > 0 && e.kv.num_blocks <= 0xffffffffll
+              ? static_cast<uint32_t>(e.kv.num_blocks - 1) : 0xffffffffu);
       uint32_t idA[NLD], idB[NLD];
       auto fetch_ids = [&](int64_t k0, uint32_t (&ids)[NLD]) __attribute__((always_inline)) {
 #pragma unroll
@@ -281,7 +284,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
                 rv, reinterpret_cast<HCP_LDS_PTR(void)>(dst + CHB + j * 1024), 16,
                 static_cast<int>(off), 0, 0, kStreamAux);
           } else {
-            const int64_t o = static_cast<int64_t>(ids[j]) * blockb + hb + inb;
+            // a block id past the cache is clamped to its last block
+            const uint32_t id = ids[j] < id_max ? ids[j] : id_max;
+            const int64_t o = static_cast<int64_t>(id) * blockb + hb + inb;
             __builtin_amdgcn_global_load_lds(
                 reinterpret_cast<const __attribute__((address_space(1))) void*>(
                     reinterpret_cast<uintptr_t>(kva.k + o)),

@@ -63,10 +63,10 @@ typedef enum hcp_dtype {
  * stride_head = bs*2D, stride_tok = 2D; file_connector.py:13-16,175-179)
  * and the vLLM 0.23 layout [nb, 2, bs, Hkv, D] (v_addr = cache + bs*Hkv*D,
  * stride_block = 2*bs*Hkv*D, stride_head = D, stride_tok = Hkv*D;
- * ring_backend.py:601,617-624).  With num_blocks given and the cache's
- * num_blocks * stride_block bytes below 4 GiB the prefill kernel reads the
- * paged segment with bounds-checked buffer loads (a block id past the cache
- * reads zeros); otherwise with plain global loads.
+ * ring_backend.py:601,617-624).  num_blocks (0: unknown) bounds the block ids
+ * the kernels read: a larger id reads the cache's last block (or, for decode
+ * over a cache under 4 GiB, zeros) instead of memory outside it.  Paged prefill needs
+ * block_size >= 16 (hcp_plan_varlen_tiles checks it).
  */
 typedef struct hcp_kv_segment {
   uint64_t k_addr;
