@@ -39,10 +39,14 @@
 //    K(n+1), V(n) and fills K(n+2), V(n+1) (both buffers free since the last
 //    barrier, so all its loads start in phase A and have phase B to land);
 //    one barrier per tile.
-//  * Lazy rescale: the running max used as the exponent reference is only
-//    raised when some row's tile max exceeds it by more than 2^8; otherwise P
-//    values are bounded by 256 and the O rescale (64 multiplies per lane) is
-//    skipped.  The result is exact: O, l and lse all use the same reference.
+//  * Lazy rescale without a per-tile max: P = exp2(c S - m_ref) is formed
+//    against the current reference (the row max of the row's first tile)
+//    together with its f32 row sum.  A lane whose 32 values of the tile sum
+//    to at most 2^12 holds no P above 2^12, and the tile goes straight to the
+//    PV MFMAs; otherwise (a score far above the reference, rare past a row's
+//    first tile) the wave takes the tile's true row max, rescales O and l,
+//    and forms P again.  The result is exact: O, l and lse all use the same
+//    reference.
 //  * Causal tiles above a wave's diagonal are skipped; masking runs only on
 //    diagonal and ragged tiles.  A ragged last tile is bounded by its buffer
 //    descriptor (rows past the segment read as zeros and are masked), so no
@@ -66,7 +70,7 @@ namespace hcp {
 #define HCP_FWD_WAVES_PER_EU 2
 #endif
 
-constexpr float kRescaleThresh = 8.0f;  // log2 units: P <= 2^8 between rescales
+constexpr float kSumThresh = 4096.0f;  // a lane's P sum over a tile: P <= 2^12 without a rescale
 // word 3 of a raw (stride 0) buffer descriptor on gfx9-family parts:
 // DATA_FORMAT = 32 bit, no swizzle, bounds checked against num_records
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -365,11 +369,11 @@ fa_fwd_kernel(FwdParams p) {
     }
 
   // ---- online softmax state ----
-  // m_ref: exponent reference of the row (log2 units), raised only when a
-  // tile's scores exceed it by more than kRescaleThresh, so P <= 2^8.
+  // m_ref: exponent reference of the row (log2 units), the row max of the
+  // first tile and raised only when a tile's P would exceed 2^12 against it
+  // (-inf until the row has seen a key).  O and l are relative to it.
   const float c = p.scale_log2;
   float m_ref = -INFINITY;
-  float thr_raw = -INFINITY;  // (m_ref + threshold) / c: the rescale test on raw scores
   float l_run = 0.f;
   f32x16 oacc[DBLK];
 #pragma unroll
@@ -433,79 +437,26 @@ fa_fwd_kernel(FwdParams p) {
     return __builtin_fmaxf(a[0], a[1]);
   };
 
-  // Lazy rescale: raise m_ref only if some row's tile max exceeds it by more
-  // than the threshold (a wave vote); the row pair (lane, lane^32) then agrees
-  // on the new reference.  O and l hold everything up to the previous tile.
-  auto check_rescale = [&](float mh) __attribute__((always_inline)) {
-    if (__any(mh > thr_raw)) {
-      const float mrow = __builtin_fmaxf(mh, __shfl_xor(mh, 32)) * c;
-      const float m_new = __builtin_fmaxf(m_ref, mrow);
-      const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
-      l_run *= alpha;
+  // Raise m_ref to the row max of a tile (mh: the lane's raw max; the row
+  // pair (lane, lane^32) agrees on it) and rescale O and l, which hold
+  // everything up to the previous tile.  Called by the whole wave.
+  auto rescale_to = [&](float mh) __attribute__((always_inline)) {
+    const float mrow = __builtin_fmaxf(mh, __shfl_xor(mh, 32)) * c;
+    const float m_new = __builtin_fmaxf(m_ref, mrow);
+    const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
+    l_run *= alpha;
 #pragma unroll
-      for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
-      m_ref = m_new;
-      // raw scores above thr_raw would give P > 2^8 against m_ref
-      thr_raw = (m_ref + kRescaleThresh) / c;
-    }
-  };
-
-  // P = exp2(c*S - m_ref), in place (fp32, kept for the row sum), and the
-  // P^T fragments in the input dtype
-  auto expo = [&](f32x16 (&S)[2]) __attribute__((always_inline)) {
-    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) S[h][r] = fast_exp2(__builtin_fmaf(S[h][r], c, -m_use));
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int b = 8 * t;
-        u32x4 w;
-        w[0] = pack2<T>(S[h][b + 0], S[h][b + 1]);
-        w[1] = pack2<T>(S[h][b + 2], S[h][b + 3]);
-        w[2] = pack2<T>(S[h][b + 4], S[h][b + 5]);
-        w[3] = pack2<T>(S[h][b + 6], S[h][b + 7]);
-        pf[2 * h + t] = as_vec8<V8>(w);
-      }
-    }
-  };
-
-  auto row_sum = [&](const f32x16 (&S)[2]) __attribute__((always_inline)) {
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      s0 += S[0][r] + S[0][r + 1];
-      s1 += S[1][r] + S[1][r + 1];
-    }
-    return s0 + s1;
-  };
-
-  // O^T += V^T P^T over the tile's 64 keys (4 steps of 16)
-  auto pv = [&](const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) {
-        const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
-        const i16x4 hi = lds_read_tr(Vs + voff[db][1] + (16 * t) * ROWB);
-        u32x4 w;
-        w[0] = __builtin_bit_cast(u32x2, lo)[0];
-        w[1] = __builtin_bit_cast(u32x2, lo)[1];
-        w[2] = __builtin_bit_cast(u32x2, hi)[0];
-        w[3] = __builtin_bit_cast(u32x2, hi)[1];
-        oacc[db] = E::mfma32(as_vec8<V8>(w), pf[t], oacc[db]);
-      }
-    }
+    for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
+    m_ref = m_new;
   };
 
   // One iteration n of the software pipeline, S_cur = scores of tile n
   // (masked, checked against m_ref), S_nxt receives tile n+1:
   //   A: S_nxt = K(n+1) Q^T            on MFMA, interleaved with
   //      P(n) = exp2(c S_cur - m_ref)  on VALU
-  //   B: O += V(n)^T P(n)^T            on MFMA, interleaved with
-  //      l += rowsum P(n), max of S_nxt on VALU
-  //   then the (rare) rescale for tile n+1.
+  //      and l += rowsum P(n)          on VALU
+  //   then the (rare) rescale of tile n, the masking of tile n+1, and
+  //   B: O += V(n)^T P(n)^T            on MFMA.
   // Each phase is one branch-free basic block (on a wave's last tile, A
   // multiplies a stale LDS tile whose result is discarded); the group
   // barriers ask the scheduler to alternate MFMA, LDS reads and VALU so the
@@ -531,26 +482,37 @@ fa_fwd_kernel(FwdParams p) {
   };
 
   // P for score pair `pair` (scores 2*pair, 2*pair+1 of the lane's 32):
-  // exp2(c S - m) in place and packed into its P^T fragment
-  auto exp_pair = [&](int pair, f32x16 (&Sc)[2], float m_use) __attribute__((always_inline)) {
+  // exp2(c S - m) packed into its P^T fragment (S is kept) and added to the
+  // lane's tile sums (two chains)
+  auto exp_pair = [&](int pair, const f32x16 (&Sc)[2], float m_use, float (&ts)[2])
+      __attribute__((always_inline)) {
     const int x = 2 * pair;  // 0..31, even
     const int h = x >> 4, r = x & 15;
     const float p0 = fast_exp2(__builtin_fmaf(Sc[h][r], c, -m_use));
     const float p1 = fast_exp2(__builtin_fmaf(Sc[h][r + 1], c, -m_use));
-    Sc[h][r] = p0;
-    Sc[h][r + 1] = p1;
     // P^T fragment 2h + (r >> 3) holds regs 8t .. 8t+7 of half h
     u32x4 w = __builtin_bit_cast(u32x4, pf[2 * h + (r >> 3)]);
-    w[(r & 7) >> 1] = pack2<T>(p0, p1);
+    const uint32_t pw = pack2<T>(p0, p1);
+    w[(r & 7) >> 1] = pw;
     pf[2 * h + (r >> 3)] = as_vec8<V8>(w);
+    ts[0] += p0;
+    ts[1] += p1;
+  };
+  // the rare path of a tile whose P would exceed 2^12 (or a row with no
+  // reference yet): rescale to the tile's true row max, form P again
+  auto redo_tile = [&](const f32x16 (&Sc)[2], float (&ts)[2]) __attribute__((always_inline)) {
+    rescale_to(tile_max(Sc));
+    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+    ts[0] = ts[1] = 0.f;
+#pragma unroll
+    for (int pr = 0; pr < 16; ++pr) exp_pair(pr, Sc, m_use, ts);
   };
   constexpr int NA = 2 * KSTEPS;  // MFMAs in phase A
   constexpr int EA = 32 / NA;     // scores exponentiated per phase-A MFMA
   constexpr int NB = 4 * DBLK;    // MFMAs in phase B
-  constexpr int EB = 32 / NB;     // scores summed / maxed per phase-B MFMA
-  auto phase_a = [&](const HCP_LDS(char)* Ks, f32x16 (&Sc)[2], f32x16 (&Sn)[2],
+  auto phase_a = [&](const HCP_LDS(char)* Ks, const f32x16 (&Sc)[2], f32x16 (&Sn)[2],
                      __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst,
-                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2)
+                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2, float (&ts)[2])
       __attribute__((always_inline)) {
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     constexpr int KR = HCP_KPF + 1;  // K fragment ring
@@ -579,7 +541,7 @@ fa_fwd_kernel(FwdParams p) {
       }
       // scores st*EA .. st*EA+EA-1 of the current tile
 #pragma unroll
-      for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, m_use);
+      for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, m_use, ts);
       __builtin_amdgcn_sched_barrier(0);
     }
     // P(n) is complete here: keep its computation in this phase (all its uses
@@ -587,47 +549,29 @@ fa_fwd_kernel(FwdParams p) {
     // otherwise move it and serialise it behind the PV MFMAs)
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pf[i]));
-    asm volatile("" : "+v"(Sc[0]), "+v"(Sc[1]));
+    asm volatile("" : "+v"(ts[0]), "+v"(ts[1]));
   };
 
   // Phase B: O += V(n)^T P(n)^T (NB MFMAs, transposing V reads two MFMAs
-  // ahead) while l gathers P(n)'s row sum and mh the raw max of S_nxt.
-  auto phase_b = [&](const HCP_LDS(char)* Vs, const f32x16 (&Sc)[2], const f32x16 (&Sn)[2],
-                     float& mh) __attribute__((always_inline)) {
+  // ahead).
+  auto phase_b = [&](const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
     u32x4 vf[VR];
     auto vread = [&](int j) __attribute__((always_inline)) { return vread_at(Vs, j); };
 #pragma unroll
     for (int j = 0; j < HCP_VPF; ++j) vf[j] = vread(j);
-    float rs0 = Sc[0][0], rs1 = Sc[0][1];
-    float m0 = Sn[0][0];
 #pragma unroll
     for (int st = 0; st < NB; ++st) {
       const int t = st / DBLK, db = st % DBLK;
       if (st + HCP_VPF < NB) vf[(st + HCP_VPF) % VR] = vread(st + HCP_VPF);
       oacc[db] = E::mfma32(as_vec8<V8>(vf[st % VR]), pf[t], oacc[db]);
-#pragma unroll
-      for (int q = 0; q < EB; q += 2) {
-        const int x = st * EB + q;
-        const int h = x >> 4, r = x & 15;
-        if (x > 0) {
-          rs0 += Sc[h][r];
-          rs1 += Sc[h][r + 1];
-        }
-        m0 = (x == 0) ? __builtin_fmaxf(m0, Sn[h][r + 1])
-                      : __builtin_fmaxf(__builtin_fmaxf(m0, Sn[h][r]), Sn[h][r + 1]);
-      }
-      // pin this step's VALU work under this step's MFMA
-      asm volatile("" : "+v"(rs0), "+v"(rs1), "+v"(m0));
       __builtin_amdgcn_sched_barrier(0);
     }
-    l_run += rs0 + rs1;
-    mh = m0;
   };
 
-  // One iteration n of the software pipeline (S_cur = scores of tile n, masked
-  // and checked against m_ref; S_nxt receives tile n+1): phase A, then the
-  // masking of tile n+1 when it is a diagonal or ragged tile, then phase B,
-  // then the (rare) rescale for tile n+1.  On a wave's last tile phase A
+  // One iteration n of the software pipeline (S_cur = scores of tile n,
+  // masked; S_nxt receives tile n+1): phase A, then the (rare) rescale of
+  // tile n, the masking of tile n+1 when it is a diagonal or ragged tile, and
+  // phase B.  On a wave's last tile phase A
   // multiplies a stale LDS tile whose result is discarded.  The four tile
   // buffers are distinct __shared__ objects so the compiler can tell the LDS
   // reads from the global->LDS writes in flight and does not wait for them.
@@ -648,11 +592,12 @@ fa_fwd_kernel(FwdParams p) {
       rsv = tile_rsrc(vseg, n + 1);
     }
     if (n < wtiles) {
-      phase_a(Ks, Sc, Sn, rsk, kload, rsv, vload);
+      float ts[2] = {0.f, 0.f};
+      phase_a(Ks, Sc, Sn, rsk, kload, rsv, vload, ts);
+      if (__any(ts[0] + ts[1] > kSumThresh || m_ref == -INFINITY)) redo_tile(Sc, ts);
+      l_run += ts[0] + ts[1];
       if (needs_mask(n + 1)) apply_mask(Sn, n + 1);
-      float mh;
-      phase_b(Vs, Sc, Sn, mh);
-      if (n + 1 < wtiles) check_rescale(mh);
+      phase_b(Vs);
     } else {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -702,7 +647,7 @@ fa_fwd_kernel(FwdParams p) {
   if (wtiles > 0) {
     qk(K0, SA);
     if (needs_mask(0)) apply_mask(SA, 0);
-    check_rescale(tile_max(SA));
+    rescale_to(tile_max(SA));
   }
   __syncthreads();  // K(0) is read by every wave before K(2) overwrites it
 
