@@ -514,6 +514,10 @@ fa_fwd_kernel(FwdParams p) {
                      __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst,
                      __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2, float (&ts)[2])
       __attribute__((always_inline)) {
+    // Phase A carries the VALU work; at raised wave priority its instructions
+    // issue ahead of the other wave on the SIMD, whose MFMAs (often its phase
+    // B) keep the matrix pipe busy meanwhile.  Phase B drops it again.
+    __builtin_amdgcn_s_setprio(1);
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     constexpr int KR = HCP_KPF + 1;  // K fragment ring
     V8 kf[KR];
@@ -556,6 +560,7 @@ fa_fwd_kernel(FwdParams p) {
   // ahead).
   auto phase_b = [&](const HCP_LDS(char)* Vs) __attribute__((always_inline)) {
     u32x4 vf[VR];
+    __builtin_amdgcn_s_setprio(0);
     auto vread = [&](int j) __attribute__((always_inline)) { return vread_at(Vs, j); };
 #pragma unroll
     for (int j = 0; j < HCP_VPF; ++j) vf[j] = vread(j);
