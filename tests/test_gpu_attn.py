@@ -4,7 +4,8 @@ Cases follow the reference's kernel probe (validate_ring_triton_kernel.py:41-61:
 six (Tq, Tk, offset) shapes, causal and non-causal, H=14 / Hkv=2 / D=64 fp16,
 gate 2e-3 on out and LSE) and repeat them at the Qwen2.5-7B attention shape
 (28 / 4 / 128) in bf16 and fp16, plus logit outliers, ragged and empty
-segments, negative offsets and strided inputs.
+segments, negative offsets, strided inputs, and scores that rise far above
+(or fall far below) a row's first tile.
 """
 
 import pytest
@@ -116,3 +117,44 @@ def test_deterministic_repeat(dev):
     a = ring_attn_with_lse(q, k, v, 0.088, 400)
     b = ring_attn_with_lse(q, k, v, 0.088, 400)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def _drift_inputs(gen, tq, tk, h, hkv, d, dtype, slope, spike):
+    """Queries and keys sharing one direction u: key j carries slope*j/64 of it
+    (scores drift by about slope log2 units per 64-key tile), and key `spike`
+    (if any) 40 more."""
+    u = torch.randn(d, generator=gen)
+    u /= u.norm()
+    q = torch.randn(tq, h, d, generator=gen) + 8.0 * u
+    w = slope * torch.arange(tk, dtype=torch.float32) / 64.0
+    if spike is not None:
+        w[spike] += 40.0
+    k = torch.randn(tk, hkv, d, generator=gen) + w[:, None, None] * u
+    v = torch.randn(tk, hkv, d, generator=gen)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("off", [None, 1500])
+@pytest.mark.parametrize("slope,spike", [(2.0, None), (-2.0, None), (0.0, 1500)])
+def test_scores_far_above_first_tile(dev, dtype, off, slope, spike):
+    """Rows whose later scores exceed their first tile's maximum by far more
+    than the exponent headroom (rising scores, one late spike) must be
+    rescaled on the way; falling scores underflow harmlessly."""
+    tq, tk, h, hkv, d = 300, 2048, 8, 2, 128
+    gen = torch.Generator().manual_seed(int(slope * 10) + 7 * (off or 0) + 3)
+    q, k, v = _drift_inputs(gen, tq, tk, h, hkv, d, dtype, slope, spike)
+    scale = scale_for(d)
+    # the inputs do exercise the rescale: against the first tile's maximum,
+    # some later score is more than 12 log2 units higher in every row
+    s = torch.einsum("qhd,khd->hqk", q.float(), k.float().repeat_interleave(h // hkv, 1))
+    s = s * scale * 1.4426950408889634
+    if off is not None:
+        s = s.masked_fill(torch.arange(tk)[None, :] > off + torch.arange(tq)[:, None], -torch.inf)
+    rise = (s.amax(-1) - s[..., :64].amax(-1)).amin().item()
+    assert (rise > 12.0) == (slope > 0 or spike is not None), rise
+    o, lse = ring_attn_with_lse(q.to(dev), k.to(dev), v.to(dev), scale, off)
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_with_lse(q.float(), k.float(), v.float(), scale, off)
+    assert max_err(o, ro) <= OUT_TOL[dtype]
+    assert max_err(lse, rl) <= LSE_TOL
