@@ -1,0 +1,106 @@
+"""GPU parity at the benchmark's full sizes.
+
+Rows of attention are independent, so sampled query rows (or sequences) of a
+full-size launch are checked exactly against the oracle run on those rows
+alone, and the whole output against a size-independent identity: the ring
+step (peer pass, then the local pass merging it, ring_backend.py:820-831)
+equals one causal pass over the concatenated keys [peer; local] with the
+queries at positions len(peer)+i.  Inputs are drawn on the device from a
+seeded generator (the bench's shapes; N(0,1), K outlier channels x8).
+"""
+
+import pytest
+import torch
+
+from hcp_vllm_plugin_amd import ring_attn_with_lse
+from hcp_vllm_plugin_amd.ring_attn import ring_attn_merged
+from hcp_vllm_plugin_amd.varlen import PagedCache, decode_attn, segment_contiguous, segment_paged
+from oracle import ring_oracle as orc
+from tests._util import LSE_TOL, OUT_TOL, max_err, scale_for
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+
+
+def _draw(g, shape, dev, outlier_ch=None):
+    x = torch.randn(*shape, generator=g, device=dev)
+    if outlier_ch is not None:
+        x[..., outlier_ch] *= 8.0
+    return x.to(BF16)
+
+
+@pytest.mark.parametrize("h,hkv,n_q,n_loc,n_peer,q0,n_out,blocks", [
+    # Qwen2.5-7B shape: 8192 local causal (frame offset 0) + 8192 peer keys
+    (28, 4, 8192, 8192, 8192, 0, 4, (0, 2047, 5000, 8176)),
+    # Llama-3-70B shape, last of the eight 8192-query chunks of a 65536-token
+    # prompt: local keys [0, 65536) causal at offset 57344, 65536 peer keys
+    (64, 8, 8192, 65536, 65536, 57344, 8, (0, 8176)),
+])
+def test_ring_prefill_step_full_size(dev, h, hkv, n_q, n_loc, n_peer, q0, n_out, blocks):
+    d = 128
+    g = torch.Generator(device=dev).manual_seed(h + n_loc)
+    ch = torch.randperm(d, generator=torch.Generator().manual_seed(h))[:n_out]
+    q = _draw(g, (n_q, h, d), dev)
+    kl, vl = _draw(g, (n_loc, hkv, d), dev, ch), _draw(g, (n_loc, hkv, d), dev)
+    kp, vp = _draw(g, (n_peer, hkv, d), dev, ch), _draw(g, (n_peer, hkv, d), dev)
+    scale = scale_for(d)
+    o_peer, lse_peer = ring_attn_with_lse(q, kp, vp, scale, None)
+    lse = torch.empty(h, n_q, dtype=torch.float32, device=dev)
+    out = ring_attn_merged(q, kl, vl, scale, q0, o_peer, lse_peer, output_lse=lse)
+    del o_peer, lse_peer
+    kk, vv = torch.cat([kp, kl]), torch.cat([vp, vl])
+    del kp, vp, kl, vl
+    o1, l1 = ring_attn_with_lse(q, kk, vv, scale, n_peer + q0)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    # both sides are within the tolerance of the exact result (checked on the
+    # sampled rows below), so they agree to twice it: two bf16 roundings of
+    # one value in [2, 4) can differ by 2^-6
+    assert max_err(out, o1) <= 2 * OUT_TOL[BF16], max_err(out, o1)
+    assert max_err(lse, l1) <= 2 * LSE_TOL, max_err(lse, l1)
+    del o1, l1
+    kc, vc = kk.float().cpu(), vv.float().cpu()
+    for r0 in blocks:
+        ro, rl = orc.attn_with_lse(q[r0:r0 + 16].float().cpu(), kc, vc, scale, n_peer + q0 + r0)
+        assert max_err(out[r0:r0 + 16], ro) <= OUT_TOL[BF16], (r0, max_err(out[r0:r0 + 16], ro))
+        assert max_err(lse[:, r0:r0 + 16], rl) <= LSE_TOL, r0
+
+
+def test_split_kv_decode_full_size(dev):
+    """64 sequences, each 32768 contiguous peer keys + U[512, 2048] local keys
+    in a paged [nb, 4, 16, 256] cache under a random block table; every
+    sequence's output goes through the full launch, eight are checked."""
+    h, hkv, d, bs, s, n_peer = 28, 4, 128, 16, 64, 32768
+    gc = torch.Generator().manual_seed(3)
+    loc = torch.randint(512, 2049, (s,), generator=gc).tolist()
+    blocks = [-(-n // bs) for n in loc]
+    nb = sum(blocks) + 4
+    perm = torch.randperm(nb, generator=gc).to(torch.int32)
+    bt = torch.zeros(s, max(blocks), dtype=torch.int32)
+    o = 0
+    for r, n in enumerate(blocks):
+        bt[r, :n] = perm[o:o + n]
+        o += n
+    g = torch.Generator(device=dev).manual_seed(3)
+    cache = _draw(g, (nb, hkv, bs, 2 * d), dev)
+    q = _draw(g, (s, h, d), dev)
+    kp, vp = _draw(g, (s * n_peer, hkv, d), dev), _draw(g, (s * n_peer, hkv, d), dev)
+    btd = bt.to(dev)
+    pc = PagedCache.from_tensor(cache)
+    segs = [[segment_contiguous(kp, vp, r * n_peer, n_peer), segment_paged(pc, btd[r], 0, loc[r])]
+            for r in range(s)]
+    scale = scale_for(d)
+    out, lse = decode_attn(q, segs, hkv, scale, with_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    cache_c = cache.float().cpu()
+    for r in range(0, s, 9):
+        kl, vl = orc.gather_paged(cache_c, bt[r], 0, loc[r], "v031")
+        qr = q[r:r + 1].float().cpu()
+        ro_l, rl_l = orc.attn_with_lse(qr, kl, vl, scale, loc[r] - 1)
+        sl = slice(r * n_peer, (r + 1) * n_peer)
+        ro_p, rl_p = orc.attn_with_lse(qr, kp[sl].float().cpu(), vp[sl].float().cpu(), scale, None)
+        ro, rl = orc.merge_pair(ro_l, rl_l, ro_p, rl_p)
+        assert max_err(out[r:r + 1], ro) <= OUT_TOL[BF16], (r, max_err(out[r:r + 1], ro))
+        assert max_err(lse[:, r:r + 1], rl) <= LSE_TOL, r
