@@ -104,3 +104,59 @@ def test_split_kv_decode_full_size(dev):
         ro, rl = orc.merge_pair(ro_l, rl_l, ro_p, rl_p)
         assert max_err(out[r:r + 1], ro) <= OUT_TOL[BF16], (r, max_err(out[r:r + 1], ro))
         assert max_err(lse[:, r:r + 1], rl) <= LSE_TOL, r
+
+
+def test_varlen_batch_full_size(dev):
+    """16 requests: local U[512, 4096] queries causal over their own keys in a
+    paged [nb, 4, 16, 256] cache (the block-table row also covers the
+    request's 16*U[64, 1024] prefix blocks, which the local pass does not
+    read), peer = the prefix keys packed contiguously.  The peer launch, then
+    the local launch merging it; four requests checked at both ends."""
+    from hcp_vllm_plugin_amd.varlen import VarlenLaunch, make_entry
+
+    h, hkv, d, bs, nreq = 28, 4, 128, 16, 16
+    gc = torch.Generator().manual_seed(2)
+    loc = torch.randint(512, 4097, (nreq,), generator=gc).tolist()
+    pre = (16 * torch.randint(64, 1025, (nreq,), generator=gc)).tolist()
+    blocks = [-(-(p + n) // bs) for p, n in zip(pre, loc)]
+    nb = sum(blocks) + 8
+    perm = torch.randperm(nb, generator=gc).to(torch.int32)
+    bt = torch.zeros(nreq, max(blocks), dtype=torch.int32)
+    o = 0
+    for r, n in enumerate(blocks):
+        bt[r, :n] = perm[o:o + n]
+        o += n
+    g = torch.Generator(device=dev).manual_seed(2)
+    cache = _draw(g, (nb, hkv, bs, 2 * d), dev)
+    q = _draw(g, (sum(loc), h, d), dev)
+    pk, pv = _draw(g, (sum(pre), hkv, d), dev), _draw(g, (sum(pre), hkv, d), dev)
+    btd = bt.to(dev)
+    pc = PagedCache.from_tensor(cache)
+    loc_e, peer_e, qs, ps = [], [], [0], [0]
+    for r in range(nreq):
+        loc_e.append(make_entry(qs[-1], loc[r], segment_paged(pc, btd[r], pre[r], loc[r]), 0))
+        peer_e.append(make_entry(qs[-1], loc[r], segment_contiguous(pk, pv, ps[-1], pre[r])))
+        qs.append(qs[-1] + loc[r])
+        ps.append(ps[-1] + pre[r])
+    scale = scale_for(d)
+    o_peer = torch.empty_like(q)
+    lse_peer = torch.empty(h, qs[-1], dtype=torch.float32, device=dev)
+    VarlenLaunch(peer_e, False, False, dev).run(q, o_peer, lse_peer, hkv, scale)
+    out = torch.empty_like(q)
+    lse = torch.empty(h, qs[-1], dtype=torch.float32, device=dev)
+    VarlenLaunch(loc_e, True, True, dev).run(q, out, lse, hkv, scale, acc=(o_peer, lse_peer))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    cache_c = cache.float().cpu()
+    for r in (0, 5, 10, 15):
+        kl, vl = orc.gather_paged(cache_c, bt[r], pre[r], loc[r], "v031")
+        kp_r = pk[ps[r]:ps[r + 1]].float().cpu()
+        vp_r = pv[ps[r]:ps[r + 1]].float().cpu()
+        for i0 in (0, loc[r] - 16):
+            rows = slice(qs[r] + i0, qs[r] + i0 + 16)
+            qr = q[rows].float().cpu()
+            ro_l, rl_l = orc.attn_with_lse(qr, kl, vl, scale, i0)
+            ro_p, rl_p = orc.attn_with_lse(qr, kp_r, vp_r, scale, None)
+            ro, rl = orc.merge_pair(ro_p, rl_p, ro_l, rl_l)
+            assert max_err(out[rows], ro) <= OUT_TOL[BF16], (r, i0, max_err(out[rows], ro))
+            assert max_err(lse[:, rows], rl) <= LSE_TOL, (r, i0)
