@@ -25,12 +25,12 @@
 //    lane 4e+a reads 4 consecutive d of key kbase+e and every lane receives 4
 //    keys of one d column.
 //  * Software pipeline over 64-key tiles: iteration n computes S(n+1) on the
-//    matrix pipe while the VALU turns S(n) into P(n) (phase A), then O +=
-//    V(n)^T P(n)^T while the VALU sums P(n) and takes the max of S(n+1)
-//    (phase B).  Each MFMA step carries its own share of VALU work and its
-//    LDS reads a few MFMAs ahead, written out in order and pinned with
-//    scheduling barriers, so the softmax runs under the MFMAs instead of
-//    between them.
+//    matrix pipe while the VALU turns S(n) into P(n) and sums it (phase A, at
+//    raised wave priority), then O += V(n)^T P(n)^T on the matrix pipe alone
+//    (phase B), while the other wave on the SIMD fills the VALU.  Each phase-A
+//    MFMA step carries its own share of VALU work, and every MFMA its LDS
+//    reads a few MFMAs ahead, written out in order and pinned with scheduling
+//    barriers, so the softmax runs under the MFMAs instead of between them.
 //  * K and V tiles (64 keys x D, row-major, 16-byte slots XOR-swizzled by
 //    2*(row&3) | (row>>2 & 1) so both the K reads and the transposing V reads
 //    are bank-conflict free) go HBM/L2 -> LDS with buffer_load ... lds (no
