@@ -71,6 +71,53 @@ def test_decode_fp16_d64(dev):
           bs=16, seed=53, split=128)
 
 
+@pytest.mark.parametrize("split", [None, 64])
+def test_decode_paged_cache_past_4gib_nan_outside_segments(dev, split):
+    """A cache of 4.6 GB (its span from a head's base exceeds 4 GiB, so the
+    split kernel loads with 64-bit addresses), the sequences' blocks past
+    4 GiB, segments starting mid-block with ragged ends, and every slot
+    outside them NaN: reading any of those would show in the result."""
+    h, hkv, d, bs = 28, 4, 128, 16
+    blk_bytes = hkv * bs * 2 * d * 2
+    nb = 4_600_000_000 // blk_bytes + 1
+    cache = torch.full((nb, hkv, bs, 2 * d), float("nan"), dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator().manual_seed(78)
+    seqs = [(37, 300), (0, 5000), (15, 1), (100, 2049)]  # (segment start, length)
+    rows, ks, vs = [], [], []
+    next_hi = nb - 1  # blocks allocated downward from the top of the cache
+    for start, ln in seqs:
+        nblk = -(-(start + ln) // bs)
+        ids = list(range(next_hi - nblk + 1, next_hi + 1))[::-1]
+        next_hi -= nblk
+        rows.append(ids)
+        k = randn(gen, (ln, hkv, d), torch.bfloat16)
+        v = randn(gen, (ln, hkv, d), torch.bfloat16)
+        pos = torch.arange(start, start + ln)
+        blk = torch.tensor(ids, dtype=torch.long)[pos // bs].to(dev)
+        slot = (pos % bs).to(dev)
+        cache[blk, :, slot, :d] = k.to(dev)
+        cache[blk, :, slot, d:] = v.to(dev)
+        ks.append(k)
+        vs.append(v)
+    assert min(min(r) for r in rows) * blk_bytes > (1 << 32)
+    bt = torch.zeros(len(seqs), max(len(r) for r in rows), dtype=torch.int32)
+    for r, ids in enumerate(rows):
+        bt[r, :len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    btd = bt.to(dev)
+    pc = PagedCache.from_tensor(cache)
+    q = randn(gen, (len(seqs), h, d), torch.bfloat16)
+    segs = [[segment_paged(pc, btd[r], start, ln)] for r, (start, ln) in enumerate(seqs)]
+    scale = scale_for(d)
+    out, lse = decode_attn(q.to(dev), segs, hkv, scale, with_lse=True, split_tokens=split)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any() and not torch.isnan(lse).any()
+    for r, (_, ln) in enumerate(seqs):
+        ro, rl = orc.attn_with_lse(q[r:r + 1].float(), ks[r].float(), vs[r].float(), scale, ln - 1)
+        assert max_err(out[r:r + 1], ro) <= OUT_TOL[torch.bfloat16], r
+        assert max_err(lse[:, r:r + 1], rl) <= LSE_TOL, r
+    del cache
+
+
 def test_decode_empty_sequence(dev):
     """A sequence whose segments are all empty gets out 0, lse -inf."""
     h, hkv, d = 28, 4, 128
