@@ -12,7 +12,7 @@ table) -- and runs one launch per segment kind:
 * ``decode_attn``: split-KV decode of single-token queries; every segment of a
   sequence (peer and local) is split, and one reduce merges all partials.
 
-Paged layouts (SURVEY of the reference): vLLM 0.31 ``[nb, Hkv, bs, 2*D]`` with
+Paged layouts the reference reads: vLLM 0.31 ``[nb, Hkv, bs, 2*D]`` with
 K in ``[..., :D]`` and V in ``[..., D:]`` (file_connector.py:13-16,175-179),
 and vLLM 0.23 ``[nb, 2, bs, Hkv, D]`` (ring_backend.py:601,617-624).
 """
