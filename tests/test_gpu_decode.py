@@ -54,16 +54,17 @@ def _case(dev, h, hkv, d, dtype, peer_lens, loc_lens, bs, seed, split):
         ps += peer_lens[r]
 
 
-@pytest.mark.parametrize("split", [None, 64, 256, 1000])
+@pytest.mark.parametrize("split", [None, 32, 64, 256, 1000])
 def test_decode_qwen7b_shape(dev, split):
     _case(dev, 28, 4, 128, torch.bfloat16,
           peer_lens=[4096, 0, 1000, 33, 2048, 7],
           loc_lens=[512, 700, 1, 2048, 33, 1500], bs=16, seed=51, split=split)
 
 
-def test_decode_llama70b_shape(dev):
+@pytest.mark.parametrize("split", [None, 16])
+def test_decode_llama70b_shape(dev, split):
     _case(dev, 64, 8, 128, torch.bfloat16, peer_lens=[3000, 100], loc_lens=[900, 17],
-          bs=16, seed=52, split=None)
+          bs=16, seed=52, split=split)
 
 
 def test_decode_fp16_d64(dev):
@@ -71,7 +72,7 @@ def test_decode_fp16_d64(dev):
           bs=16, seed=53, split=128)
 
 
-@pytest.mark.parametrize("split", [None, 64])
+@pytest.mark.parametrize("split", [None, 16, 64])
 def test_decode_paged_cache_past_4gib_nan_outside_segments(dev, split):
     """A cache of 4.6 GB (its span from a head's base exceeds 4 GiB, so the
     split kernel loads with 64-bit addresses), the sequences' blocks past
