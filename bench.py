@@ -134,6 +134,8 @@ def bench_prefill(dev, steps, warmup, two_step=True):
 
 
 def decode_inputs(dev, seed=3, seqs=64, peer_len=32768, bs=16):
+    from hcp_vllm_plugin_amd.ring_backend import head_major
+
     gen = torch.Generator().manual_seed(seed)
     loc = torch.randint(512, 2049, (seqs,), generator=gen).tolist()
     blocks = [-(-l // bs) for l in loc]
@@ -143,6 +145,8 @@ def decode_inputs(dev, seed=3, seqs=64, peer_len=32768, bs=16):
     cache = torch.randn(nb, HKV, bs, 2 * D, generator=dgen, device=dev).to(torch.bfloat16)
     pk = torch.randn(seqs * peer_len, HKV, D, generator=dgen, device=dev).to(torch.bfloat16)
     pv = torch.randn(seqs * peer_len, HKV, D, generator=dgen, device=dev).to(torch.bfloat16)
+    # the peer prefix as stage_peer_kv stores staged chunks: head-major
+    pk, pv = head_major(pk), head_major(pv)
     q = torch.randn(seqs, H, D, generator=gen).to(torch.bfloat16).to(dev)
     perm = torch.randperm(nb, generator=gen).to(torch.int32)
     bt = torch.zeros(seqs, max(blocks), dtype=torch.int32)
@@ -754,7 +758,7 @@ def main():
     }
     if dec is not None:
         line["decode"] = {
-            "workload": "split-KV decode: 64 seqs x (32768 peer + U[512,2048] paged local)",
+            "workload": "split-KV decode: 64 seqs x (32768 peer staged head-major + U[512,2048] paged local)",
             "ms": round(dec["ms"], 4),
             "value": round(dec["gbs"], 1),
             "unit": "GB/s",
