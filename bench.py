@@ -134,7 +134,7 @@ def bench_prefill(dev, steps, warmup, two_step=True):
 
 
 def decode_inputs(dev, seed=3, seqs=64, peer_len=32768, bs=16):
-    from hcp_vllm_plugin_amd.ring_backend import head_major
+    from hcp_vllm_plugin_amd.varlen import head_major
 
     gen = torch.Generator().manual_seed(seed)
     loc = torch.randint(512, 2049, (seqs,), generator=gen).tolist()

@@ -57,6 +57,7 @@ from .merge import merge_attn_states
 from .ring_attn import ring_attn_with_lse
 from .ring_decode import GrowthBuffer, growth_assignee, local_partial, ring_decode_step
 from .varlen import (
+    head_major,
     DecodeBatch,
     PagedCache,
     VarlenLaunch,
@@ -97,15 +98,6 @@ except ImportError:  # vLLM absent: same surface, no base classes
 # ---------------------------------------------------------------------------
 PEER_KV_STAGING: dict[tuple[str, str], tuple[torch.Tensor, torch.Tensor]] = {}
 PEER_REQ_MAP: dict[int, list[str]] = {}
-
-
-def head_major(t: torch.Tensor) -> torch.Tensor:
-    """``t`` (``[n, Hkv, D]``) as an ``[n, Hkv, D]`` view of an ``[Hkv, n, D]``
-    buffer, so each KV head's keys are one contiguous run (returned as is if
-    already so stored)."""
-    if t.dim() != 3 or t.stride() == (t.shape[2], t.shape[0] * t.shape[2], 1):
-        return t
-    return t.permute(1, 0, 2).contiguous().permute(1, 0, 2)
 
 
 def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Tensor) -> None:

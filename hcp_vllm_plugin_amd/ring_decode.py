@@ -42,7 +42,7 @@ import torch
 from .packet import Packet, encode, replace
 from .packet import _NAMES as _DTYPE_NAMES
 from .peer_ingest import PeerIngest
-from .varlen import DecodeBatch, decode_attn, segment_contiguous
+from .varlen import DecodeBatch, decode_attn, head_major, segment_contiguous
 
 logger = logging.getLogger(__name__)
 
@@ -291,9 +291,10 @@ class RingDecodeNode:
         self._ready.set()
 
     def add_chunk(self, chunk_key: str, layer: str, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Install one layer of a chunk snapshot (``[n, Hkv, D]`` each)."""
-        k = k.to(self._device, self._dtype)
-        v = v.to(self._device, self._dtype)
+        """Install one layer of a chunk snapshot (``[n, Hkv, D]`` each), stored
+        head-major like staged peer KV: installed once, read at every hop."""
+        k = head_major(k.to(self._device, self._dtype))
+        v = head_major(v.to(self._device, self._dtype))
         self._layers[(chunk_key, layer)] = (k, v)
 
     def mark_ready(self) -> None:

@@ -38,6 +38,7 @@ __all__ = [
     "DecodeBatch",
     "decode_attn",
     "choose_split_tokens",
+    "head_major",
 ]
 
 
@@ -399,6 +400,15 @@ def varlen_attn_with_lse(
                          device=q.device)
     VarlenLaunch(entries, causal, paged, q.device).run(q, out, lse, num_kv_heads, scale, window)
     return out, lse
+
+
+def head_major(t: torch.Tensor) -> torch.Tensor:
+    """``t`` (``[n, Hkv, D]``) as an ``[n, Hkv, D]`` view of an ``[Hkv, n, D]``
+    buffer, so each KV head's keys are one contiguous run (returned as is if
+    already so stored)."""
+    if t.dim() != 3 or t.stride() == (t.shape[2], t.shape[0] * t.shape[2], 1):
+        return t
+    return t.permute(1, 0, 2).contiguous().permute(1, 0, 2)
 
 
 def choose_split_tokens(seg_lens: list[int], num_kv_heads: int, num_cus: int = 256,
