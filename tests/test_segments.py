@@ -9,7 +9,7 @@ own chunk + growth + current token).
 import pytest
 import torch
 
-from hcp_vllm_plugin_amd.varlen import segment_contiguous, trim_segment, window_tail
+from hcp_vllm_plugin_amd.varlen import head_major, segment_contiguous, trim_segment, window_tail
 
 
 def _segs():
@@ -47,3 +47,26 @@ def test_trim_segment_keeps_the_descriptor():
     assert trim_segment(a, 40).len == 0
     with pytest.raises(ValueError):
         trim_segment(a, 41)
+
+
+def test_head_major_view_and_staging():
+    """Staged peer KV keeps its values and [n, Hkv, D] shape but is stored
+    head-major (each KV head's keys one contiguous run); a tensor already so
+    stored is returned as is, and a segment over it carries the strides."""
+    from hcp_vllm_plugin_amd import ring_backend as rb
+
+    k = torch.randn(37, 4, 16)
+    h = head_major(k)
+    assert h.shape == k.shape and torch.equal(h, k)
+    assert h.stride() == (16, 37 * 16, 1) and h.is_contiguous() is False
+    assert head_major(h) is h
+    seg = segment_contiguous(h, h, 5, 20)
+    assert (seg.stride_tok, seg.stride_head) == (16, 37 * 16)
+    v = torch.randn(37, 4, 16)
+    try:
+        rb.stage_peer_kv("c0", "layer0", k, v)
+        sk, sv = rb.PEER_KV_STAGING[("c0", "layer0")]
+        assert torch.equal(sk, k) and torch.equal(sv, v)
+        assert sk.stride() == (16, 37 * 16, 1) and sv.stride() == (16, 37 * 16, 1)
+    finally:
+        rb.clear_peer_kv()
