@@ -576,7 +576,8 @@ def cpu_baseline(budget_s=30.0):
     """
     from oracle import ring_oracle as orc
 
-    threads = min(16, os.cpu_count() or 1)
+    host = cpu_host_info()
+    threads = host["threads"]
     torch.set_num_threads(threads)
     q, kl, vl, kp, vp = (t.float() for t in prefill_inputs(torch.device("cpu")))
     n, g = q.shape[0], H // HKV
@@ -602,12 +603,59 @@ def cpu_baseline(budget_s=30.0):
         "value": flops / t / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
+        "threads": threads,
+        "cpu_model": host["cpu_model"],
+        "physical_cores": host["physical_cores"],
+        "logical_cpus": host["logical_cpus"],
+        "cpus_granted": host["cpus_granted"],
         "kind": "port",
         "sample": (f"the full prefill step (8192 local causal + 8192 peer + merge, 28/4 heads) "
                    f"on the CPU oracle (torch fp32), one KV-head group at a time; "
                    f"{flops / 1e12:.3f} TFLOP in {t:.2f} s, median of {len(times)} steps, "
-                   f"{threads} threads"),
+                   f"{threads} threads ({host['threads_rule']})"),
     }
+
+
+def cpu_host_info() -> dict:
+    """The host CPU as the CPU baseline uses it.
+
+    ``threads`` is every CPU this process may run on (its affinity set, which
+    is what ``os.cpu_count()`` means for it), capped by ``OMP_NUM_THREADS``
+    when the machine sets one: a GPU host shared by several GPU jobs grants
+    each its CPU share that way.  Model and physical-core count come from
+    /proc/cpuinfo (unique (physical id, core id) pairs)."""
+    logical = os.cpu_count() or 1
+    try:
+        granted = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        granted = logical
+    threads, rule = granted, "all CPUs granted to the process"
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < granted:
+        threads, rule = int(omp), f"the host's CPU share OMP_NUM_THREADS={omp} of {granted} granted"
+    model, cores = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            phys = core = None
+            for ln in f:
+                k, _, v = ln.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+            if phys is not None:
+                cores.add((phys, core))
+    except OSError:
+        pass
+    return {"threads": threads, "threads_rule": rule, "cpu_model": model,
+            "physical_cores": len(cores) or None, "logical_cpus": logical,
+            "cpus_granted": granted}
 
 
 def copy_probe(dev, mib=1024, reps=3):

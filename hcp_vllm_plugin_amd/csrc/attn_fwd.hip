@@ -45,8 +45,14 @@
 //    to at most 2^12 holds no P above 2^12, and the tile goes straight to the
 //    PV MFMAs; otherwise (a score far above the reference, rare past a row's
 //    first tile) the wave takes the tile's true row max, rescales O and l,
-//    and forms P again.  The result is exact: O, l and lse all use the same
-//    reference.
+//    and forms P again.  O, l and lse all use the same reference.
+//  * Two row sums: l of P in f32 gives the LSE, and lr of P as rounded to
+//    the input dtype for the PV product (v_dot2 against (1, 1)) normalises
+//    O.  Against a lazy reference a dominant key's P is 2^x with fractional x
+//    (the reference kernel's running max gives it exactly 1), whose rounding
+//    would shift the output by up to 2^-8 of that key's V; normalising by the
+//    sum of the same rounded weights cancels it, keeping the output error at
+//    the reference kernel's level.
 //  * Causal tiles above a wave's diagonal are skipped; masking runs only on
 //    diagonal and ragged tiles.  A ragged last tile is bounded by its buffer
 //    descriptor (rows past the segment read as zeros and are masked), so no
@@ -374,7 +380,8 @@ fa_fwd_kernel(FwdParams p) {
   // (-inf until the row has seen a key).  O and l are relative to it.
   const float c = p.scale_log2;
   float m_ref = -INFINITY;
-  float l_run = 0.f;
+  float l_run = 0.f;   // sum of P in f32: the LSE
+  float lr_run = 0.f;  // sum of P as rounded for the PV product: normalises O
   f32x16 oacc[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) oacc[i] = f32x16{};
@@ -445,6 +452,7 @@ fa_fwd_kernel(FwdParams p) {
     const float m_new = __builtin_fmaxf(m_ref, mrow);
     const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
     l_run *= alpha;
+    lr_run *= alpha;
 #pragma unroll
     for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
     m_ref = m_new;
@@ -484,7 +492,7 @@ fa_fwd_kernel(FwdParams p) {
   // P for score pair `pair` (scores 2*pair, 2*pair+1 of the lane's 32):
   // exp2(c S - m) packed into its P^T fragment (S is kept) and added to the
   // lane's tile sums (two chains)
-  auto exp_pair = [&](int pair, const f32x16 (&Sc)[2], float m_use, float (&ts)[2])
+  auto exp_pair = [&](int pair, const f32x16 (&Sc)[2], float m_use, float (&ts)[4])
       __attribute__((always_inline)) {
     const int x = 2 * pair;  // 0..31, even
     const int h = x >> 4, r = x & 15;
@@ -497,13 +505,14 @@ fa_fwd_kernel(FwdParams p) {
     pf[2 * h + (r >> 3)] = as_vec8<V8>(w);
     ts[0] += p0;
     ts[1] += p1;
+    ts[2 + (pair & 1)] = sum2<T>(pw, ts[2 + (pair & 1)]);
   };
   // the rare path of a tile whose P would exceed 2^12 (or a row with no
   // reference yet): rescale to the tile's true row max, form P again
-  auto redo_tile = [&](const f32x16 (&Sc)[2], float (&ts)[2]) __attribute__((always_inline)) {
+  auto redo_tile = [&](const f32x16 (&Sc)[2], float (&ts)[4]) __attribute__((always_inline)) {
     rescale_to(tile_max(Sc));
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-    ts[0] = ts[1] = 0.f;
+    ts[0] = ts[1] = ts[2] = ts[3] = 0.f;
 #pragma unroll
     for (int pr = 0; pr < 16; ++pr) exp_pair(pr, Sc, m_use, ts);
   };
@@ -512,7 +521,7 @@ fa_fwd_kernel(FwdParams p) {
   constexpr int NB = 4 * DBLK;    // MFMAs in phase B
   auto phase_a = [&](const HCP_LDS(char)* Ks, const f32x16 (&Sc)[2], f32x16 (&Sn)[2],
                      __amdgpu_buffer_rsrc_t rs, HCP_LDS(char)* ldst,
-                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2, float (&ts)[2])
+                     __amdgpu_buffer_rsrc_t rs2, HCP_LDS(char)* ldst2, float (&ts)[4])
       __attribute__((always_inline)) {
     // Phase A carries the VALU work; at raised wave priority its instructions
     // issue ahead of the other wave on the SIMD, whose MFMAs (often its phase
@@ -553,7 +562,7 @@ fa_fwd_kernel(FwdParams p) {
     // otherwise move it and serialise it behind the PV MFMAs)
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pf[i]));
-    asm volatile("" : "+v"(ts[0]), "+v"(ts[1]));
+    asm volatile("" : "+v"(ts[0]), "+v"(ts[1]), "+v"(ts[2]), "+v"(ts[3]));
   };
 
   // Phase B: O += V(n)^T P(n)^T (NB MFMAs, transposing V reads two MFMAs
@@ -597,10 +606,11 @@ fa_fwd_kernel(FwdParams p) {
       rsv = tile_rsrc(vseg, n + 1);
     }
     if (n < wtiles) {
-      float ts[2] = {0.f, 0.f};
+      float ts[4] = {0.f, 0.f, 0.f, 0.f};
       phase_a(Ks, Sc, Sn, rsk, kload, rsv, vload, ts);
       if (__any(ts[0] + ts[1] > kSumThresh || m_ref == -INFINITY)) redo_tile(Sc, ts);
       l_run += ts[0] + ts[1];
+      lr_run += ts[2] + ts[3];
       if (needs_mask(n + 1)) apply_mask(Sn, n + 1);
       phase_b(Vs);
     } else {
@@ -614,7 +624,10 @@ fa_fwd_kernel(FwdParams p) {
       id_v = id_k;
       id_k = id_f;
     }
-    __syncthreads();  // waits for this iteration's tile loads (vmcnt(0)) first
+    // This iteration's tile loads land in LDS that other waves read next
+    // iteration: each wave drains its own DMA, then the barrier publishes it.
+    wait_vmcnt<0>();
+    __syncthreads();
   };
 
   HCP_LDS(char)* K0 = (HCP_LDS(char)*)(bufK0);
@@ -648,6 +661,7 @@ fa_fwd_kernel(FwdParams p) {
       if (ntiles > 1) issue(kseg, 1, K1);
     }
   }
+  wait_vmcnt<0>();  // the prologue tiles (and Q) have landed before the barrier
   __syncthreads();
   if (wtiles > 0) {
     qk(K0, SA);
@@ -666,6 +680,7 @@ fa_fwd_kernel(FwdParams p) {
 
   // ---- epilogue ----
   const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float lr_tot = lr_run + __shfl_xor(lr_run, 32);
   // Merge path: this wave's 32 rows of the partial state are fetched whole
   // (coalesced) into the wave's share of the tile buffers, free since the
   // loop's last barrier.  Load instruction i fills bytes [i*1024, +1024) of
@@ -697,7 +712,7 @@ fa_fwd_kernel(FwdParams p) {
     }
   }
   if (q_valid) {
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float inv = lr_tot > 0.f ? 1.f / lr_tot : 0.f;
     const int64_t row = e.q_start + qi;
     char* orow = reinterpret_cast<char*>(p.out) +
                  (row * p.o_stride_tok + static_cast<int64_t>(head) * p.o_stride_head) * 2;

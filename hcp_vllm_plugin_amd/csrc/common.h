@@ -81,6 +81,21 @@ __device__ __forceinline__ uint32_t pack2<_Float16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), f16x2));
 }
 
+// acc + lo + hi of a dword of two 16-bit elements, in f32: one v_dot2_f32_*
+// against (1, 1), so the sum is of the rounded values themselves.
+template <typename T>
+__device__ __forceinline__ float sum2(uint32_t w, float acc);
+template <>
+__device__ __forceinline__ float sum2<__bf16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                         __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+}
+template <>
+__device__ __forceinline__ float sum2<_Float16>(uint32_t w, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w),
+                                __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
+}
+
 template <typename V>
 __device__ __forceinline__ V as_vec8(u32x4 x) {
   return __builtin_bit_cast(V, x);

@@ -343,6 +343,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
   }
 
   // ---- combine the 4 waves (the chunk buffers are reused for O) ----
+  // Each wave's last prefetch (issued unconditionally in the loop) may still
+  // be writing bufE/bufO, which sm_o overlays: drain it before the barrier.
+  wait_vmcnt<0>();
   __syncthreads();
   float (*sm_o)[16][D] = reinterpret_cast<float (*)[16][D]>(&bufE[0][0]);
   float l_tot = l_run + __shfl_xor(l_run, 16);

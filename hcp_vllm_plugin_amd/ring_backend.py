@@ -98,23 +98,66 @@ except ImportError:  # vLLM absent: same surface, no base classes
 # ---------------------------------------------------------------------------
 PEER_KV_STAGING: dict[tuple[str, str], tuple[torch.Tensor, torch.Tensor]] = {}
 PEER_REQ_MAP: dict[int, list[str]] = {}
+# (chunk_key, layer_name) -> (event recorded after the staged copy was queued,
+# streams already ordered after it); a forward on any stream waits on the
+# event once before reading the chunk
+_STAGE_READY: dict[tuple[str, str], tuple[torch.cuda.Event, set]] = {}
 
 
-def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Tensor) -> None:
+def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Tensor,
+                  ready: torch.cuda.Event | None = None) -> None:
     """Stage a peer chunk's K/V ``[n, Hkv, D]`` (post-RoPE) for one layer.
 
     Stored head-major (one copy per chunk and layer): a chunk is staged once
     and read by every decode step, and the split-KV decode streams a KV head's
     keys 5% faster as one contiguous run than as rows interleaved with the
     other heads'; the prefill passes read either layout at the same rate.
+
+    Ordering: the copy is queued on the caller's current stream.  ``ready``
+    (e.g. ``IngestedKV.event`` of a ``PeerIngest.load`` on a side stream) is
+    waited on by that stream first, so the copy reads landed bytes.  An event
+    recorded after the copy is kept with the entry and every forward that
+    reads the chunk makes its own stream wait on it, so staging from a
+    connector thread's stream and reading from the model's stream is ordered
+    on the device without a host synchronisation.
     """
-    PEER_KV_STAGING[(chunk_key, layer_name)] = (head_major(k), head_major(v))
+    on_gpu = k.is_cuda
+    if on_gpu and ready is not None:
+        torch.cuda.current_stream(k.device).wait_event(ready)
+    key = (chunk_key, layer_name)
+    PEER_KV_STAGING[key] = (head_major(k), head_major(v))
+    if on_gpu:
+        st = torch.cuda.current_stream(k.device)
+        ev = torch.cuda.Event()
+        ev.record(st)
+        _STAGE_READY[key] = (ev, {st})
+    else:
+        _STAGE_READY.pop(key, None)
+
+
+def _wait_staged(key: tuple[str, str], kv: tuple[torch.Tensor, torch.Tensor]) -> None:
+    """Order the current stream after the staging copy of ``key`` (once per
+    stream).  A chunk staged on another stream is also marked as used on this
+    one, so the caching allocator keeps its memory until this stream's reads
+    are done even if the chunk is dropped meanwhile."""
+    ent = _STAGE_READY.get(key)
+    if ent is None:
+        return
+    ev, seen = ent
+    cur = torch.cuda.current_stream(kv[0].device)
+    if cur in seen:
+        return
+    cur.wait_event(ev)
+    for t in kv:
+        t.record_stream(cur)
+    seen.add(cur)
 
 
 def drop_chunk_kv(chunk_key: str) -> int:
     keys = [key for key in PEER_KV_STAGING if key[0] == chunk_key]
     for key in keys:
         del PEER_KV_STAGING[key]
+        _STAGE_READY.pop(key, None)
     return len(keys)
 
 
@@ -136,6 +179,7 @@ def request_peer_chunk(first_block_id: int) -> list[str] | None:
 def clear_peer_kv() -> None:
     PEER_KV_STAGING.clear()
     PEER_REQ_MAP.clear()
+    _STAGE_READY.clear()
 
 
 # ---------------------------------------------------------------------------
@@ -490,6 +534,8 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
                     "falling back to local path", ck_list, layer_name)
                 return None
             parts.append(kv)
+        for ck, kv in zip(ck_list, parts):
+            _wait_staged((ck, layer_name), kv)
         return parts
 
     def _plan(self, layer_name, qsl, seq_lens, block_table, first_blocks, pc, split):

@@ -353,6 +353,15 @@ class RingDecodeNode:
     def _accumulate_into(self, q, o_acc, lse_acc, scale, layer, req, chunk, out, lse) -> None:
         my_chunk = self._chunk_keys[0] if self._chunk_keys else chunk
         k, v = self._layers[(my_chunk, layer)]
+        # the packet's q sets the kernel's row width and head count: it must
+        # match this node's KV, or the kernel would read rows of another width
+        if q.dim() != 3 or q.shape[2] != k.shape[2] or q.shape[1] % k.shape[1] != 0:
+            raise ValueError(
+                f"decode-ring packet q {tuple(q.shape)} does not match this node's KV "
+                f"[n, {k.shape[1]}, {k.shape[2]}] (head_dim must agree, heads a multiple "
+                f"of the KV heads)")
+        if tuple(o_acc.shape) != tuple(q.shape) or tuple(lse_acc.shape) != (q.shape[1], q.shape[0]):
+            raise ValueError("decode-ring packet o/lse shapes do not match q")
         g = self._growth.get((req, layer))
         glen = g.len if g is not None else 0
         sig = (k.data_ptr(), k.shape[0], g.k.data_ptr() if glen else 0, glen, tuple(q.shape))

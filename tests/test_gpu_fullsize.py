@@ -33,8 +33,11 @@ def _draw(g, shape, dev, outlier_ch=None):
 @pytest.mark.parametrize("h,hkv,n_q,n_loc,n_peer,q0,n_out,blocks", [
     # Qwen2.5-7B shape: 8192 local causal (frame offset 0) + 8192 peer keys
     (28, 4, 8192, 8192, 8192, 0, 4, (0, 2047, 5000, 8176)),
-    # Llama-3-70B shape, last of the eight 8192-query chunks of a 65536-token
-    # prompt: local keys [0, 65536) causal at offset 57344, 65536 peer keys
+    # Llama-3-70B shape, chunks 0, 3 and 7 of the eight 8192-query chunks of
+    # a 65536-token prompt: chunk c sees local keys [0, 8192(c+1)) causal at
+    # offset 8192c, and all 65536 peer keys
+    (64, 8, 8192, 8192, 65536, 0, 8, (0, 8176)),
+    (64, 8, 8192, 32768, 65536, 24576, 8, (0, 4000, 8176)),
     (64, 8, 8192, 65536, 65536, 57344, 8, (0, 8176)),
 ])
 def test_ring_prefill_step_full_size(dev, h, hkv, n_q, n_loc, n_peer, q0, n_out, blocks):
@@ -67,10 +70,16 @@ def test_ring_prefill_step_full_size(dev, h, hkv, n_q, n_loc, n_peer, q0, n_out,
         assert max_err(lse[:, r0:r0 + 16], rl) <= LSE_TOL, r0
 
 
-def test_split_kv_decode_full_size(dev):
+@pytest.mark.parametrize("peer_layout", ["head_major", "token_major"])
+def test_split_kv_decode_full_size(dev, peer_layout):
     """64 sequences, each 32768 contiguous peer keys + U[512, 2048] local keys
     in a paged [nb, 4, 16, 256] cache under a random block table; every
-    sequence's output goes through the full launch, eight are checked."""
+    sequence's output goes through the full launch, eight are checked.  The
+    peers are stored head-major ([Hkv, n, D] behind the [n, Hkv, D] view, as
+    stage_peer_kv stores staged chunks: 64-bit head offsets of up to 3.7 GB)
+    or token-major (as loaded)."""
+    from hcp_vllm_plugin_amd.varlen import head_major
+
     h, hkv, d, bs, s, n_peer = 28, 4, 128, 16, 64, 32768
     gc = torch.Generator().manual_seed(3)
     loc = torch.randint(512, 2049, (s,), generator=gc).tolist()
@@ -86,6 +95,9 @@ def test_split_kv_decode_full_size(dev):
     cache = _draw(g, (nb, hkv, bs, 2 * d), dev)
     q = _draw(g, (s, h, d), dev)
     kp, vp = _draw(g, (s * n_peer, hkv, d), dev), _draw(g, (s * n_peer, hkv, d), dev)
+    if peer_layout == "head_major":
+        kp, vp = head_major(kp), head_major(vp)
+        assert kp.stride() == (d, s * n_peer * d, 1)
     btd = bt.to(dev)
     pc = PagedCache.from_tensor(cache)
     segs = [[segment_contiguous(kp, vp, r * n_peer, n_peer), segment_paged(pc, btd[r], 0, loc[r])]
