@@ -27,6 +27,9 @@ HCP_EUNSUPPORTED = -2
 HCP_ELAUNCH = -3
 HCP_EWORKSPACE = -4
 
+# include/hcp_mi355x.h HCP_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
 DTYPE_F32 = 2
@@ -54,11 +57,12 @@ EXPORTED_SYMBOLS = (
     "hcp_decode_workspace_bytes",
     "hcp_decode_splitkv",
     "hcp_decode_splitkv_acc",
+    "hcp_decode_splitkv_noalloc",
     "hcp_merge_attn_states",
     "hcp_reshape_and_cache",
 )
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class KvSegment(ctypes.Structure):
@@ -169,6 +173,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_decode_splitkv_acc.argtypes = [
         _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I32, _P, ctypes.c_size_t,
         _P, _I64, _I64, _P, _I64,
+        _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _F, _I32, _P,
+    ]
+    lib.hcp_decode_splitkv_noalloc.restype = ctypes.c_int
+    lib.hcp_decode_splitkv_noalloc.argtypes = [
+        _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I32,
         _P, _I64, _I64, _P, _I64, _I32, _I32, _I32, _F, _I32, _P,
     ]
     lib.hcp_reshape_and_cache.restype = ctypes.c_int

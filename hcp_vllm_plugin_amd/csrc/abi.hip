@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <numeric>
 #include <vector>
 
@@ -460,6 +461,75 @@ int hcp_decode_splitkv_acc(const void* q, int64_t q_stride_tok, int64_t q_stride
                      o_stride_tok, o_stride_head, lse, lse_stride_head, acc_o, acc_stride_tok,
                      acc_stride_head, acc_lse, acc_lse_stride_head, num_heads, num_kv_heads,
                      head_dim, scale, dtype, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split partials live in this file-scope device
+// array instead of a caller workspace.  In host code `scratch` names a
+// host-side stand-in, not device memory: its per-device address comes from
+// hipGetSymbolAddress (once per device, with that device current) and only
+// that address is ever passed to a kernel.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[HCP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (resolved on the first
+// call there).
+int scratch_on_current_device(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HCP_ELAUNCH, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(HCP_EUNSUPPORTED, "%s: device index %d beyond %d", who, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(HCP_ELAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HCP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hcp_decode_splitkv_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                               const hcp_varlen_entry* entries, int32_t num_entries,
+                               const hcp_decode_split* splits, int32_t num_splits,
+                               const int32_t* seq_partial_start, int32_t num_seqs, void* out,
+                               int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+                               int64_t lse_stride_head, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, float scale, int32_t dtype, void* stream) {
+  const char* who = "hcp_decode_splitkv_noalloc";
+  int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
+  if (rc) return rc;
+  if (num_splits < 0 || num_seqs < 0) return fail(HCP_EINVAL, "%s: negative counts", who);
+  const size_t need = hcp_decode_workspace_bytes(num_splits, num_heads, head_dim);
+  if (need > HCP_NOALLOC_SCRATCH_BYTES)
+    return fail(HCP_EWORKSPACE,
+                "%s: %d splits x %d heads x head_dim %d need %zu bytes of partials; the "
+                "library's fixed scratch holds %zu (use hcp_decode_splitkv with a workspace, "
+                "or plan fewer splits)",
+                who, num_splits, num_heads, head_dim, need,
+                static_cast<size_t>(HCP_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  if (num_splits > 0 && num_seqs > 0 && (rc = scratch_on_current_device(&ws, who))) return rc;
+  return decode_impl(who, q, q_stride_tok, q_stride_head, entries, num_entries, splits,
+                     num_splits, seq_partial_start, num_seqs, ws, HCP_NOALLOC_SCRATCH_BYTES, out,
+                     o_stride_tok, o_stride_head, lse, lse_stride_head, nullptr, 0, 0, nullptr,
+                     0, num_heads, num_kv_heads, head_dim, scale, dtype, stream);
 }
 
 int hcp_merge_attn_states(void* out, int64_t o_stride_tok, int64_t o_stride_head,

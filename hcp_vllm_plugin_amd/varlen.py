@@ -516,12 +516,34 @@ class DecodeBatch:
         return self
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
-            scale: float, acc: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+            scale: float, acc: tuple[torch.Tensor, torch.Tensor] | None = None,
+            noalloc: bool = False) -> None:
         """Decode into ``out`` (and ``lse``).  With ``acc = (o_acc [S, H, D] in
         q's dtype, lse_acc [H, S] float32)`` the accumulator is merged in by the
         same launch (``hcp_decode_splitkv_acc``); ``out`` / ``lse`` may be the
-        accumulator's own tensors."""
+        accumulator's own tensors.
+
+        ``noalloc``: run ``hcp_decode_splitkv_noalloc`` instead, whose partials
+        live in the library's fixed per-GPU scratch (no workspace is taken, so
+        nothing is allocated; calls overlapping on one GPU race).  Plans whose
+        partials exceed ``_lib.NOALLOC_SCRATCH_BYTES`` raise."""
         L = _lib.lib()
+        if noalloc:
+            if acc is not None:
+                raise ValueError("noalloc decode has no accumulator form")
+            with torch.cuda.device(q.device):
+                rc = L.hcp_decode_splitkv_noalloc(
+                    q.data_ptr(), q.stride(0), q.stride(1),
+                    self.entries_ptr, self.num_entries,
+                    self.splits_ptr, self.num_splits,
+                    self.starts_ptr, self.num_seqs,
+                    out.data_ptr(), out.stride(0), out.stride(1),
+                    lse.data_ptr() if lse is not None else None,
+                    lse.stride(0) if lse is not None else 0,
+                    self.num_heads, self.num_kv_heads, self.head_dim, float(scale),
+                    _lib.dtype_code(q.dtype), _lib.stream_ptr(q.device))
+            _lib.check(rc, "hcp_decode_splitkv_noalloc")
+            return
         # fp32 partials: stream-ordered scratch from torch's caching allocator
         workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=q.device)
         head = (q.data_ptr(), q.stride(0), q.stride(1),

@@ -5,7 +5,9 @@
  * Conventions shared by every entry point
  *   - All tensors are caller-owned device memory passed as raw pointers (or as
  *     64-bit device addresses inside descriptors).  The library never
- *     allocates device memory and keeps no pointer after a call returns.
+ *     allocates device memory and keeps no pointer after a call returns; its
+ *     only device memory is the fixed scratch array of
+ *     hcp_decode_splitkv_noalloc, part of its code object.
  *   - Strides are in ELEMENTS of the tensor's own dtype.  The last dimension
  *     (head_dim) must be contiguous.
  *   - Every launch is asynchronous on `stream` (a hipStream_t, NULL = default
@@ -34,7 +36,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 7
+#define HCP_ABI_VERSION 8
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -305,6 +307,43 @@ int hcp_decode_splitkv_acc(const void* q, int64_t q_stride_tok,
                            int32_t num_heads, int32_t num_kv_heads,
                            int32_t head_dim, float scale, int32_t dtype,
                            void* stream);
+
+/*
+ * Bytes of the library's own decode scratch on each GPU (the fp32 split
+ * partials of hcp_decode_splitkv_noalloc): 16 MiB, i.e. up to 1161 splits at
+ * 28 query heads and head_dim 128.
+ */
+#define HCP_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/*
+ * hcp_decode_splitkv without a caller workspace and without any allocation:
+ * the split partials go to a fixed device array inside the library
+ * (HCP_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends).  No
+ * counterpart in the reference: it is for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Arguments as hcp_decode_splitkv minus the workspace; a plan
+ * whose hcp_decode_workspace_bytes exceeds HCP_NOALLOC_SCRATCH_BYTES is
+ * rejected with HCP_EWORKSPACE before anything is launched.  Every call on a
+ * GPU shares that GPU's scratch and leaves its partials there (nothing in it
+ * needs to start at zero: each split writes its slot before the reduce reads
+ * it), so calls that overlap on one GPU -- on different streams, or from
+ * different threads without ordering -- race; calls on one stream do not.
+ * The first call on a device (with that device current) resolves the array's
+ * address there; later calls reuse it.
+ */
+int hcp_decode_splitkv_noalloc(const void* q, int64_t q_stride_tok,
+                               int64_t q_stride_head,
+                               const hcp_varlen_entry* entries,
+                               int32_t num_entries,
+                               const hcp_decode_split* splits,
+                               int32_t num_splits,
+                               const int32_t* seq_partial_start,
+                               int32_t num_seqs, void* out,
+                               int64_t o_stride_tok, int64_t o_stride_head,
+                               float* lse, int64_t lse_stride_head,
+                               int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, float scale, int32_t dtype,
+                               void* stream);
 
 /*
  * LSE merge of two partial attentions over disjoint key sets:

@@ -293,6 +293,31 @@ def test_decode_splitkv_acc_status_codes(L):
     assert _dec_acc(L, seqs=0) == _lib.HCP_OK              # nothing to do, nothing launched
 
 
+def test_decode_noalloc_limit_and_status_codes(L):
+    """The allocation-free decode's scratch limit is the header's, and plans
+    beyond it (and bad arguments) are refused before any HIP call."""
+    src = open(HEADER).read()
+    m = re.search(r"#define HCP_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", src)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+
+    def call(splits=8, seqs=1, h=28, hkv=4, d=128, dtype=_lib.DTYPE_BF16):
+        return L.hcp_decode_splitkv_noalloc(16, 128 * h, 128, 16, 1, 16, splits, 16, seqs,
+                                            16, 128 * h, 128, None, 0, h, hkv, d, 0.1, dtype,
+                                            None)
+
+    # largest split count that fits: partials + LSE, 256-byte aligned
+    fit = max(n for n in range(1, 2000)
+              if L.hcp_decode_workspace_bytes(n, 28, 128) <= _lib.NOALLOC_SCRATCH_BYTES)
+    assert fit == 1161
+    assert call(splits=fit + 1) == _lib.HCP_EWORKSPACE
+    assert b"fixed scratch" in L.hcp_last_error()
+    assert call(d=96) == _lib.HCP_EUNSUPPORTED
+    assert call(h=30) == _lib.HCP_EINVAL
+    assert call(dtype=_lib.DTYPE_F32) == _lib.HCP_EUNSUPPORTED
+    assert call(splits=-1) == _lib.HCP_EINVAL
+    assert call(seqs=0) == _lib.HCP_OK  # nothing to do: no device touched
+
+
 def _cache_desc(bs=16, nb=4):
     c = _lib.PagedCacheDesc()
     c.k_addr, c.v_addr = 0x1000, 0x1100
