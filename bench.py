@@ -199,6 +199,94 @@ def bench_decode(dev, steps, warmup):
     }
 
 
+def bench_decode_forward(dev, steps, warmup, seqs=64, peer_len=32768, bs=16, seed=3,
+                         layers=4):
+    """The batch-64 split-KV decode as the backend runs it:
+    ``HcpRingAttentionImpl.forward`` on one decode step of 64 requests whose
+    32768-token prefixes are staged peer chunks (``stage_peer_kv`` +
+    ``map_request_peer``, one chunk per request and layer) and whose
+    U[512, 2048] local tokens are in the paged cache (the block-table rows also
+    cover the prefix, whose pool slots the reference never reads: they point
+    at one spare block).  Decode-ring off (``HCP_RING_DECODE_RING=0``).
+    ``forward_ms`` is the per-layer call over ``layers`` layers of one step
+    (metadata shared, as vLLM passes it); ``kernel_ms`` the same launch alone."""
+    import types
+
+    from hcp_vllm_plugin_amd import ring_backend as rb
+    from hcp_vllm_plugin_amd.varlen import (DecodeBatch, PagedCache, segment_contiguous,
+                                            segment_paged)
+
+    os.environ["HCP_RING_DECODE_RING"] = "0"
+    gen = torch.Generator().manual_seed(seed)
+    loc = torch.randint(512, 2049, (seqs,), generator=gen).tolist()
+    pre_blocks = peer_len // bs
+    blocks = [-(-n // bs) for n in loc]
+    nb = sum(blocks) + 1  # block 0: the prefix slots' spare block
+    dgen = torch.Generator(device=dev).manual_seed(seed)
+    caches = [torch.randn(nb, HKV, bs, 2 * D, generator=dgen, device=dev).to(torch.bfloat16)
+              for _ in range(layers)]
+    perm = (torch.randperm(nb - 1, generator=gen) + 1).to(torch.int32)
+    bt = torch.zeros(seqs, pre_blocks + max(blocks), dtype=torch.int32)
+    o = 0
+    for r, nbk in enumerate(blocks):
+        bt[r, pre_blocks:pre_blocks + nbk] = perm[o:o + nbk]
+        o += nbk
+    bt = bt.to(dev)
+    q = torch.randn(seqs, H, D, generator=gen).to(torch.bfloat16).to(dev)
+    # staged chunks as stage_peer_kv stores them: [n, Hkv, D] views of
+    # head-major [Hkv, n, D] storage (stage_peer_kv keeps them without a copy)
+    rb.clear_peer_kv()
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(layers)]
+    stash = []
+    for li, name in enumerate(names):
+        pk = torch.randn(seqs, HKV, peer_len, D, generator=dgen, device=dev).to(torch.bfloat16)
+        pv = torch.randn(seqs, HKV, peer_len, D, generator=dgen, device=dev).to(torch.bfloat16)
+        stash.append((pk, pv))
+        for r in range(seqs):
+            rb.stage_peer_kv(f"req{r}-prefix", name, pk[r].permute(1, 0, 2), pv[r].permute(1, 0, 2))
+    # a request is known by its first block id (ring_backend.py:740-754): the
+    # prefix blocks are never read, so each row's first entry is its own id
+    bt[:, 0] = torch.arange(1000, 1000 + seqs, dtype=torch.int32, device=dev)
+    for r in range(seqs):
+        rb.map_request_peer(1000 + r, [f"req{r}-prefix"])
+    meta = types.SimpleNamespace(
+        num_actual_tokens=seqs,
+        query_start_loc=torch.arange(seqs + 1, dtype=torch.int32, device=dev),
+        seq_lens=torch.tensor([peer_len + n for n in loc], dtype=torch.int32, device=dev),
+        block_table=bt)
+    impl = rb.HcpRingAttentionImpl(H, D, SCALE, HKV)
+    out = torch.empty_like(q)
+    layer_objs = [types.SimpleNamespace(layer_name=n) for n in names]
+
+    def step():
+        for li in range(layers):
+            impl.forward(layer_objs[li], q, None, None, caches[li], meta, out)
+
+    rb.reset_impl_stats()
+    ms_step = timed(step, steps, warmup)
+    assert rb.IMPL_STATS["decode_hip"] > 0 and rb.IMPL_STATS["attn_torch"] == 0
+    # the same launch alone: layer 0's segments
+    pc = PagedCache.from_tensor(caches[0])
+    pk, pv = stash[0]
+    segs = [[segment_paged(pc, bt[r], peer_len, loc[r]),
+             segment_contiguous(pk[r].permute(1, 0, 2), pv[r].permute(1, 0, 2))]
+            for r in range(seqs)]
+    batch = DecodeBatch(segs, H, HKV, D, dev)
+    ms_kernel = timed(lambda: batch.run(q, out, None, SCALE), steps, warmup)
+    rb.clear_peer_kv()
+    del stash, caches
+    byts = (seqs * peer_len + sum(loc)) * HKV * D * 2 * 2 + seqs * H * D * 2 * 2
+    fwd = ms_step / layers
+    return {
+        "workload": (f"batch-{seqs} decode through HcpRingAttentionImpl.forward: {peer_len}-token "
+                     f"staged peer prefix per request (stage_peer_kv + map_request_peer) + "
+                     f"U[512,2048] paged local, {layers} layers of one step"),
+        "forward_ms": round(fwd, 4), "kernel_ms": round(ms_kernel, 4),
+        "forward_over_kernel": round(fwd / ms_kernel, 4),
+        "gbs_forward": round(byts / (fwd * 1e-3) / 1e9, 1), "bytes": byts,
+    }
+
+
 def bench_decode_paged(dev, steps, warmup, seqs=64, keys=34000, bs=16, seed=7):
     """Serving decode with every key in the paged cache (no peer): 64 requests
     of 34000 keys, the layer's cache [nb, 4, 16, 256] bf16 of 4.46 GB (past
@@ -694,7 +782,7 @@ def main():
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
                                        "kvwrite", "ingest", "ringdec", "window", "pdecode",
-                                       "copy"),
+                                       "fdecode", "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -720,6 +808,9 @@ def main():
         return
     if args.part == "ingest":
         print(json.dumps(bench_peer_ingest(dev, args.steps, args.warmup)), flush=True)
+        return
+    if args.part == "fdecode":
+        print(json.dumps(bench_decode_forward(dev, args.steps, args.warmup)), flush=True)
         return
     if args.part == "pdecode":
         print(json.dumps(bench_decode_paged(dev, args.steps, args.warmup)), flush=True)
@@ -750,6 +841,7 @@ def main():
         extra["ring_decode_hop"] = bench_ring_decode_hop(dev, args.steps, args.warmup)
         extra["sliding_window"] = bench_sliding_window(dev, args.steps, args.warmup)
         extra["decode_paged"] = bench_decode_paged(dev, args.steps, args.warmup)
+        extra["decode_forward_staged"] = bench_decode_forward(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 

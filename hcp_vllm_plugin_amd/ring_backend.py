@@ -57,6 +57,7 @@ from .merge import merge_attn_states
 from .ring_attn import ring_attn_with_lse
 from .ring_decode import GrowthBuffer, growth_assignee, local_partial, ring_decode_step
 from .varlen import (
+    ENTRY_DTYPE,
     head_major,
     DecodeBatch,
     PagedCache,
@@ -243,6 +244,17 @@ def _release_staged_for_request(first_block_id: int) -> None:
     else:
         for ck in PEER_REQ_MAP.pop(first_block_id, None) or []:
             drop_chunk_kv(ck)
+
+
+def _contiguous_record(j: int, seq: int, k: torch.Tensor, v: torch.Tensor):
+    """hcp_varlen_entry of decode query row ``seq`` over all of a staged chunk
+    (contiguous k/v ``[n, Hkv, D]``), as an ENTRY_DTYPE record value."""
+    if k.stride() != v.stride() or k.data_ptr() % 16 or v.data_ptr() % 16 or \
+            (k.stride(0) * k.element_size()) % 16 or (k.stride(1) * k.element_size()) % 16 or \
+            not 0 < k.stride(0) < (1 << 24):
+        raise ValueError(f"staged chunk of entry {j}: k/v layout not loadable")
+    return (seq, 1, 0, k.data_ptr(), v.data_ptr(), 0, k.stride(0), k.stride(1), 0, 0,
+            int(k.shape[0]), 0, 0)
 
 
 # Host copy of the step's attention metadata.  vLLM hands every layer the same
@@ -626,8 +638,12 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
             self._forward_local_only(query, out, qsl, seq_lens, block_table, pc, kv_cache)
             return output
 
-        plan = self._plan(layer_name, qsl, seq_lens, block_table, first_blocks, pc, split)
         is_decode = n > 0 and qsl == list(range(n + 1))
+        if is_decode and self._forward_decode_staged(query, out, seq_lens, block_table,
+                                                     first_blocks, pc, kv_cache, layer_name,
+                                                     ring_on, split):
+            return output
+        plan = self._plan(layer_name, qsl, seq_lens, block_table, first_blocks, pc, split)
         ring_local = self._ring_local_segments(plan, pc, key, value, layer_name)
         if is_decode:
             lse = self._forward_decode(query, out, plan, n, ring_local)
@@ -718,6 +734,95 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         if not PEER_KV_STAGING:
             return True
         return n > 1 and not any(fb in PEER_REQ_MAP for fb in first_blocks)
+
+    # -- pure decode batches with staged peers ------------------------------------
+    def _decode_staged_template(self, seq_lens, block_table, first_blocks, pc, layer_name):
+        """The step's decode entries with every field that does not change
+        from layer to layer (lengths, block-table rows, strides of the cache),
+        the split plan over them, and where each layer's addresses go; False
+        if some request's staging is incomplete (the general path then
+        decides, per layer, as the reference does)."""
+        n = len(seq_lens)
+        w = self.sliding_window
+        seq, kinds, rows, starts, lens, peers = [], [], [], [], [], []
+        for r in range(n):
+            tk = int(seq_lens[r])
+            staged = None
+            if _ring_enabled():
+                staged = self._peer_for_request(first_blocks[r], layer_name, n)
+                if staged is None and PEER_REQ_MAP.get(first_blocks[r]):
+                    return False  # staging still arriving: decided per layer
+            peer_end = min(sum(int(kv[0].shape[0]) for kv in staged), tk) if staged else 0
+            # one query at position tk - 1 (ring_backend.py:626-627): inside the
+            # prefix it sees the whole local range (:811-817), else the local
+            # keys past the prefix plus every staged chunk (:820-830)
+            lo = 0 if peer_end == 0 or peer_end >= tk else peer_end
+            if w is not None:  # the causal pass sees the last `w` local keys
+                lo = max(lo, tk - w)
+            seq.append(r); kinds.append(0); rows.append(r); starts.append(lo); lens.append(tk - lo)
+            if 0 < peer_end < tk:
+                ck_list = PEER_REQ_MAP.get(first_blocks[r])
+                if ck_list is None:  # the single-request fallback of _peer_for_request
+                    ck_list = [next(iter({key[0] for key in PEER_KV_STAGING}))]
+                for ck, (kk, _vv) in zip(ck_list, staged):
+                    if kk.shape[0] > 0:
+                        seq.append(r); kinds.append(1); rows.append(r); starts.append(0)
+                        lens.append(int(kk.shape[0]))
+                        peers.append((len(seq) - 1, ck, int(kk.shape[0])))
+        m = len(seq)
+        kinds = np.asarray(kinds)
+        loc = np.nonzero(kinds == 0)[0]
+        tmpl = np.zeros(m, dtype=ENTRY_DTYPE)
+        tmpl["q_start"] = seq
+        tmpl["q_len"] = 1
+        tmpl["start"] = starts
+        tmpl["len"] = lens
+        if len(loc):
+            tmpl[loc] = paged_entry_array(pc, block_table, np.asarray(rows)[loc], tmpl["q_start"][loc],
+                                          1, 0, tmpl["start"][loc], tmpl["len"][loc])
+        first = tmpl.copy()
+        for j, ck, _nt in peers:
+            k, v = PEER_KV_STAGING[(ck, layer_name)]
+            first[j] = _contiguous_record(j, seq[j], k, v)
+        batch = DecodeBatch.from_entries(first, self.num_heads, self.num_kv_heads, self.head_size,
+                                         block_table.device, entry_seq=np.asarray(seq, np.int32),
+                                         num_seqs=n)
+        return {"tmpl": tmpl, "loc": loc, "peers": peers, "batch": batch}
+
+    def _forward_decode_staged(self, query, out, seq_lens, block_table, first_blocks, pc,
+                               kv_cache, layer_name, ring_on, split) -> bool:
+        """A pure decode batch without decode-ring rows: one split-KV launch
+        over every request's local paged segment and staged peer chunks, its
+        split plan built once per step and reused by every layer, each layer
+        writing only its addresses (the cache, the layer's staged chunks) into
+        the entries and uploading them in one small copy.  False when the
+        general path must run (split env, decode-ring rows, staging that
+        differs from the step's template)."""
+        if split > 0 or (_decode_ring_enabled() and DECODE_RING_MAP
+                         and any(fb in DECODE_RING_MAP for fb in first_blocks)):
+            return False
+        key = ("dec_staged", self.sliding_window, pc.layout, pc.stride_tok, pc.stride_head,
+               pc.stride_block, pc.block_size, pc.num_blocks, pc.v_addr - pc.k_addr, ring_on)
+        st = _STEP["fast"].get(key)
+        if st is None:
+            st = self._decode_staged_template(seq_lens, block_table, first_blocks, pc, layer_name)
+            _STEP["fast"][key] = st
+        if st is False:
+            return False
+        ent = st["tmpl"].copy()
+        ent["k_addr"][st["loc"]] = pc.k_addr
+        ent["v_addr"][st["loc"]] = pc.v_addr
+        keep = [kv_cache, block_table]
+        for j, ck, nt in st["peers"]:
+            kv = PEER_KV_STAGING.get((ck, layer_name))
+            if kv is None or int(kv[0].shape[0]) != nt:
+                return False
+            _wait_staged((ck, layer_name), kv)
+            ent[j] = _contiguous_record(j, int(ent["q_start"][j]), kv[0], kv[1])
+            keep.append(kv)
+        st["batch"].rebind(ent, keep).run(query, out, None, self.scale)
+        _count("decode")
+        return True
 
     def _forward_local_only(self, query, out, qsl, seq_lens, block_table, pc, kv_cache):
         """Causal attention of every request over its paged KV, the batch's

@@ -481,26 +481,39 @@ class DecodeBatch:
     @classmethod
     def from_entries(cls, entries: np.ndarray, num_heads: int, num_kv_heads: int,
                      head_dim: int, device: torch.device, split_tokens: int | None = None,
-                     keep=None) -> "DecodeBatch":
-        """One entry per sequence (sequence i = entry i = query row i) given as
-        an ENTRY_DTYPE array; ``keep`` holds the tensors it points into."""
+                     keep=None, entry_seq: np.ndarray | None = None,
+                     num_seqs: int | None = None) -> "DecodeBatch":
+        """Entries given as an ENTRY_DTYPE array; ``keep`` holds the tensors
+        it points into.  By default one entry per sequence (sequence i = entry
+        i = query row i); with ``entry_seq`` (int32, non-decreasing) entry j
+        belongs to sequence ``entry_seq[j]`` of ``num_seqs`` -- a sequence's
+        peer chunks and its local segment."""
         if entries.dtype != ENTRY_DTYPE or not entries.flags.c_contiguous:
             raise ValueError("entry array must be contiguous ENTRY_DTYPE")
         L = _lib.lib()
         self = cls.__new__(cls)
         n = len(entries)
-        self.num_seqs = n
+        if entry_seq is None:
+            seq_arr = np.arange(max(n, 1), dtype=np.int32)
+            ns = n
+        else:
+            seq_arr = np.ascontiguousarray(entry_seq, dtype=np.int32)
+            if len(seq_arr) != n or num_seqs is None:
+                raise ValueError("entry_seq needs one sequence per entry and num_seqs")
+            ns = int(num_seqs)
+            if n == 0:
+                seq_arr = np.zeros(1, dtype=np.int32)
+        self.num_seqs = ns
         self.num_entries = n
         lens = entries["len"]
         if split_tokens is None:
             split_tokens = choose_split_tokens([int(lens.sum())], num_kv_heads)
         self.split_tokens = split_tokens
         arr = entries if n else np.zeros(1, dtype=ENTRY_DTYPE)
-        seq_arr = np.arange(max(n, 1), dtype=np.int32)
         cap = int(((lens + split_tokens - 1) // split_tokens).sum())
         splits = (DecodeSplit * max(cap, 1))()
-        starts = (ctypes.c_int32 * (n + 1))()
-        rc = L.hcp_plan_decode_splits(arr.ctypes.data, n, seq_arr.ctypes.data, n, 0,
+        starts = (ctypes.c_int32 * (ns + 1))()
+        rc = L.hcp_plan_decode_splits(arr.ctypes.data, n, seq_arr.ctypes.data, ns, 0,
                                       split_tokens, ctypes.addressof(splits), cap,
                                       ctypes.addressof(starts))
         _lib.check(rc, "hcp_plan_decode_splits")
@@ -514,6 +527,21 @@ class DecodeBatch:
         self.device = device
         self._keep = keep
         return self
+
+    def rebind(self, entries: np.ndarray, keep=None) -> "DecodeBatch":
+        """The same plan (splits, partial slots) over new entries of the same
+        layout and lengths -- another layer's cache and staged chunks: only
+        the entries go to the device (one small asynchronous copy)."""
+        if entries.dtype != ENTRY_DTYPE or not entries.flags.c_contiguous:
+            raise ValueError("entry array must be contiguous ENTRY_DTYPE")
+        if len(entries) != self.num_entries:
+            raise ValueError("rebind needs the plan's entry count")
+        other = object.__new__(type(self))
+        other.__dict__.update(self.__dict__)
+        arr = entries if len(entries) else np.zeros(1, dtype=ENTRY_DTYPE)
+        other._entries_dev, (other.entries_ptr,) = _upload([arr], self.device)
+        other._keep = keep
+        return other
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
             scale: float, acc: tuple[torch.Tensor, torch.Tensor] | None = None,

@@ -192,3 +192,48 @@ def test_backend_type_contract():
         rb.HcpRingAttentionImpl(H, D, 0.1, HKV, alibi_slopes=[0.1] * H)
     with pytest.raises(NotImplementedError):
         rb.HcpRingAttentionImpl(H, D, 0.1, HKV, logits_soft_cap=30.0)
+
+
+@pytest.mark.parametrize("window", [None, 300])
+def test_forward_decode_staged_plan_across_layers(dev, window):
+    """A pure decode step over three layers (one metadata object, as vLLM
+    passes it): the split plan is built at the first layer and reused, each
+    layer binding its own cache and its own staged chunks.  Requests: one
+    staged chunk, two chunks, none, and a prefix at least as long as the
+    context (its query sees the local range only, ring_backend.py:811-817)."""
+    gen = torch.Generator().manual_seed(91)
+    reqs = [(1, 1024 + 300), (1, 64 + 128 + 40), (1, 700), (1, 256)]
+    chunks = [[1024], [64, 128], None, [256, 512]]
+    seq_lens = [tk for _, tk in reqs]
+    qsl = list(range(len(reqs) + 1))
+    nb = sum(-(-tk // BS) for tk in seq_lens) + 4
+    bt = _block_table(gen, seq_lens, nb)
+    meta = _meta(dev, qsl, seq_lens, bt)
+    impl = rb.HcpRingAttentionImpl(H, D, scale_for(D), HKV, sliding_window=window)
+    for li in range(3):
+        layer = types.SimpleNamespace(layer_name=f"model.layers.{li}.self_attn.attn")
+        cache = _cache(gen, "v031", nb, torch.bfloat16)
+        query = randn(gen, (len(reqs), H, D), torch.bfloat16)
+        peers = []
+        for r, cl in enumerate(chunks):
+            if not cl:
+                peers.append(None)
+                continue
+            ks, vs, keys = [], [], []
+            for c, n in enumerate(cl):
+                k, v = randn(gen, (n, HKV, D), torch.bfloat16), randn(gen, (n, HKV, D), torch.bfloat16)
+                rb.stage_peer_kv(f"r{r}c{c}", layer.layer_name, k.to(dev), v.to(dev))
+                keys.append(f"r{r}c{c}")
+                ks.append(k)
+                vs.append(v)
+            rb.map_request_peer(int(bt[r, 0]), keys)
+            peers.append((torch.cat(ks).float(), torch.cat(vs).float()))
+        out = torch.full((len(reqs), H, D), 7.0, dtype=torch.bfloat16, device=dev)
+        impl.forward(layer, query.to(dev), None, None, cache.to(dev), meta, out)
+        torch.cuda.synchronize()
+        ref = orc.ring_forward(query.float(), cache.float(), "v031", qsl, seq_lens, bt,
+                               scale_for(D), peers=peers, out_dtype=torch.float32,
+                               window=window)
+        assert max_err(out, ref) <= OUT_TOL[torch.bfloat16], li
+    assert rb.IMPL_STATS["decode_hip"] == 3
+    assert sum(1 for k in rb._STEP["fast"] if k[0] == "dec_staged") == 1
