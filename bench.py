@@ -389,9 +389,26 @@ def bench_varlen(dev, steps, warmup, seed=2, nreq=16, bs=16):
     o_loc, o_peer, out = (torch.empty_like(q) for _ in range(3))
     lse_loc = torch.empty(H, tq, device=dev)
     lse_peer = torch.empty(H, tq, device=dev)
+    # the same local keys gathered into contiguous [T, Hkv, D] tensors (set-up,
+    # outside every timed region): the paged launch's contiguous counterpart
+    kc_parts, vc_parts, locc_e = [], [], []
+    for r in range(nreq):
+        tok = torch.arange(pre[r], pre[r] + loc[r], device=dev)
+        blk = bt[r][tok // bs].long()
+        kc_parts.append(cache[blk, :, tok % bs, :D])
+        vc_parts.append(cache[blk, :, tok % bs, D:])
+    kc, vc = torch.cat(kc_parts).contiguous(), torch.cat(vc_parts).contiguous()
+    qs = cs = 0
+    for r in range(nreq):
+        locc_e.append(make_entry(qs, loc[r], segment_contiguous(kc, vc, cs, loc[r]), 0))
+        qs += loc[r]
+        cs += loc[r]
+    c_launch = VarlenLaunch(locc_e, True, False, dev)
     t_peer = timed(lambda: p_launch.run(q, o_peer, lse_peer, HKV, SCALE), steps, warmup)
     t_loc = timed(lambda: l_launch.run(q, out, None, HKV, SCALE, acc=(o_peer, lse_peer)),
                   steps, warmup)
+    t_loc_c = timed(lambda: c_launch.run(q, o_loc, None, HKV, SCALE, acc=(o_peer, lse_peer)),
+                    steps, warmup)
     # the two-step form: plain local launch and the separate merge
     t_loc_plain = timed(lambda: l_launch.run(q, o_loc, lse_loc, HKV, SCALE), steps, warmup)
     t_merge = timed(lambda: merge_attn_states(out, o_peer, lse_peer, o_loc, lse_loc),
@@ -409,6 +426,9 @@ def bench_varlen(dev, steps, warmup, seed=2, nreq=16, bs=16):
         "ms": round(t, 4), "tflops": round(tf, 2), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
         "local_paged_merged": {"ms": round(t_loc, 4),
                                "tflops": round(f_l / (t_loc * 1e-3) / 1e12, 2)},
+        "local_contiguous_merged": {"ms": round(t_loc_c, 4),
+                                    "tflops": round(f_l / (t_loc_c * 1e-3) / 1e12, 2),
+                                    "paged_tflops_over_contiguous": round(t_loc_c / t_loc, 4)},
         "peer": {"ms": round(t_peer, 4), "tflops": round(f_p / (t_peer * 1e-3) / 1e12, 2)},
         "two_step": {"local_paged_ms": round(t_loc_plain, 4), "merge_ms": round(t_merge, 4),
                      "ms": round(t_loc_plain + t_peer + t_merge, 4)},

@@ -167,13 +167,14 @@ fa_fwd_kernel(FwdParams p) {
       e.causal_offset -= lo;
     }
   }
-  // Paged segments are tiled from a 64-key boundary of the request's block
-  // frame: with block_size >= 16 each wave's rows of a tile then lie in one
-  // block.  The `lead` keys in front of the segment load as zeros and are
-  // masked for every row.
+  // Paged segments are tiled from a 16-key boundary of the request's block
+  // frame: a wave's 16 rows of a tile then start on a multiple of 16 and,
+  // with block_size >= 16, lie in one block.  The `lead` (< 16) keys in front
+  // of the segment load as zeros and are masked for every row; a segment
+  // that starts on a block boundary has none.
   int lead = 0;
   if constexpr (PAGED) {
-    lead = static_cast<int>(e.kv.start & (BN - 1));
+    lead = static_cast<int>(e.kv.start & (kFwdPagedMinBlock - 1));
     e.kv.start -= lead;
     e.kv.len += lead;
     e.causal_offset += lead;
@@ -261,32 +262,43 @@ fa_fwd_kernel(FwdParams p) {
     goff[i] = static_cast<uint32_t>(PAGED ? lrow(i) - wave * WROWS : lrow(i)) * rowb32 +
               lchunk(i) * 16u;
 
-  // paged: block id of the wave's rows of tile t (clamped to the last tile,
-  // and to the segment's last key, so the block-table read stays in the
-  // request's row).  A vector load: a scalar one would share lgkmcnt with the
-  // LDS operand reads and serialise their waits.
-  auto fetch_id = [&](int t) __attribute__((always_inline)) {
+  // paged: block ids of the wave's rows, a window of 64 tiles per VGPR (lane
+  // l holds the id of tile base + l, clamped to the last tile and to the
+  // segment's last key, so the block-table read stays in the request's row;
+  // an id past the cache is clamped to its last block).  One vector load per
+  // 64 tiles, issued a window ahead; a tile's id is then a v_readlane into an
+  // SGPR, with no memory access in the tile loop.
+  auto load_ids = [&](int t0) __attribute__((always_inline)) {
     uint32_t id = 0;
     if constexpr (PAGED) {
+      int t = t0 + lane;
       t = t < ntiles ? t : ntiles - 1;
       int key = t * BN + wave * WROWS;
       key = key < kv_len ? key : kv_len - 1;
-      int idx = static_cast<int>((e.kv.start + key) >> bs_shift);
-      asm volatile("" : "+v"(idx));
+      const int idx = static_cast<int>((e.kv.start + key) >> bs_shift);
       id = static_cast<uint32_t>(bt[idx]);
+      if (e.kv.num_blocks > 0 && id >= static_cast<uint32_t>(e.kv.num_blocks))
+        id = static_cast<uint32_t>(e.kv.num_blocks - 1);
     }
     return id;
+  };
+  uint32_t ids_cur = 0, ids_nxt = 0;  // windows [id_base, +64) and [id_base + 64, +64)
+  int id_base = 0;
+  auto tile_id = [&](int t) __attribute__((always_inline)) {
+    t = t < ntiles ? t : ntiles - 1;
+    const int rel = t - id_base;  // 0 .. 127
+    const uint32_t a = __builtin_amdgcn_readlane(ids_cur, rel & 63);
+    const uint32_t b = __builtin_amdgcn_readlane(ids_nxt, rel & 63);
+    return rel < 64 ? a : b;
   };
   // paged: descriptor of the wave's rows of tile t (clamped to the last
   // tile), based at its first row; num_records ends at the segment's last key
   // and at the block's end, so nothing past either is read (those rows read
-  // as zeros: unused cache slots may hold NaNs).  A block id past the cache
-  // is clamped to its last block.
-  auto page_rsrc = [&](const char* seg, uint32_t id_v, int t) __attribute__((always_inline)) {
+  // as zeros: unused cache slots may hold NaNs).  The rows start on a
+  // multiple of 16 of the block frame (the segment start is aligned down to
+  // 16 keys), so with block_size >= 16 all WROWS = 16 of them lie in the block.
+  auto page_rsrc = [&](const char* seg, uint32_t id, int t) __attribute__((always_inline)) {
     t = t < ntiles ? t : ntiles - 1;
-    uint32_t id = __builtin_amdgcn_readfirstlane(id_v);
-    if (e.kv.num_blocks > 0 && id >= static_cast<uint64_t>(e.kv.num_blocks))
-      id = static_cast<uint32_t>(e.kv.num_blocks - 1);
     const int r0 = t * BN + wave * WROWS;
     const int in_blk = static_cast<int>((e.kv.start + r0) & bs_mask);
     int rows = kv_len - r0;
@@ -346,9 +358,6 @@ fa_fwd_kernel(FwdParams p) {
   };
   auto load_one = [&](__amdgpu_buffer_rsrc_t rs, int i, HCP_LDS(char)* dst)
       __attribute__((always_inline)) { load_at(rs, goff[i], i, dst); };
-  // paged: block ids of the wave's rows of tiles n+1 (V), n+2 (K) and n+3
-  // (fetched during iteration n, used two iterations later)
-  uint32_t id_v = 0, id_k = 0, id_f = 0;
   // phase A issues one K or V load instruction every kLoadEvery/2 MFMAs
   constexpr int kLoadEvery = 4;
 
@@ -598,9 +607,13 @@ fa_fwd_kernel(FwdParams p) {
     // segment are clamped to its last one: they fill a buffer nobody reads.
     __amdgpu_buffer_rsrc_t rsk, rsv;
     if constexpr (PAGED) {
-      rsk = page_rsrc(kseg, id_k, n + 2);  // id fetched two iterations ago
-      rsv = page_rsrc(vseg, id_v, n + 1);
-      id_f = fetch_id(n + 3);
+      if (n + 1 >= id_base + 64) {  // V's tile left the window: slide it
+        id_base += 64;
+        ids_cur = ids_nxt;
+        ids_nxt = load_ids(id_base + 64);
+      }
+      rsk = page_rsrc(kseg, tile_id(n + 2), n + 2);
+      rsv = page_rsrc(vseg, tile_id(n + 1), n + 1);
     } else {
       rsk = tile_rsrc(kseg, n + 2);
       rsv = tile_rsrc(vseg, n + 1);
@@ -620,10 +633,6 @@ fa_fwd_kernel(FwdParams p) {
         load_one(rsv, i, vload);
       }
     }
-    if constexpr (PAGED) {
-      id_v = id_k;
-      id_k = id_f;
-    }
     // This iteration's tile loads land in LDS that other waves read next
     // iteration: each wave drains its own DMA, then the barrier publishes it.
     wait_vmcnt<0>();
@@ -638,9 +647,9 @@ fa_fwd_kernel(FwdParams p) {
   // ---- prologue: K(0), K(1), V(0) in flight; S(0) = K(0) Q^T ----
   if (ntiles > 0) {
     if constexpr (PAGED) {
-      const uint32_t id0 = fetch_id(0);
-      id_v = fetch_id(1);  // V(1), issued in iteration 0
-      id_k = fetch_id(2);  // K(2), issued in iteration 0
+      ids_cur = load_ids(0);
+      ids_nxt = load_ids(64);
+      const uint32_t id0 = tile_id(0);
       // tile 0: the alignment lead's rows read as zeros (an offset past any
       // num_records), whatever the cache holds there
       const __amdgpu_buffer_rsrc_t rk0 = page_rsrc(kseg, id0, 0), rv0 = page_rsrc(vseg, id0, 0);
@@ -651,7 +660,7 @@ fa_fwd_kernel(FwdParams p) {
         load_at(rv0, o, i, V0);
       }
       if (ntiles > 1) {
-        const __amdgpu_buffer_rsrc_t rk1 = page_rsrc(kseg, id_v, 1);
+        const __amdgpu_buffer_rsrc_t rk1 = page_rsrc(kseg, tile_id(1), 1);
 #pragma unroll
         for (int i = 0; i < NI; ++i) load_one(rk1, i, K1);
       }
