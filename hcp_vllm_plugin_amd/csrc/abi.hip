@@ -34,8 +34,9 @@ int check_heads(int32_t h, int32_t hkv, int32_t d, int32_t dtype, const char* wh
   if (h <= 0 || hkv <= 0) return fail(HCP_EINVAL, "%s: num_heads/num_kv_heads must be > 0", who);
   if (h % hkv != 0)
     return fail(HCP_EINVAL, "%s: num_heads (%d) not a multiple of num_kv_heads (%d)", who, h, hkv);
-  if (d != 64 && d != 128)
-    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d not supported (64 or 128)", who, d);
+  if (d < 8 || d > 128 || d % 8)
+    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d not supported (a multiple of 8 up to 128)",
+                who, d);
   if (!dtype16(dtype)) return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
   return HCP_OK;
 }
@@ -135,6 +136,7 @@ static int fwd_lse_impl(const char* who, const void* q, const void* k, const voi
   p.num_heads = num_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;
+  p.head_dim = head_dim;
   p.scale_log2 = scale * hcp::kLog2e;
   p.num_tiles = static_cast<int32_t>((tq + hcp::kFwdBM - 1) / hcp::kFwdBM);
   p.single.q_start = 0;
@@ -272,6 +274,7 @@ static int fwd_varlen_impl(const char* who, const void* q, int64_t q_stride_tok,
   p.num_heads = num_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;
+  p.head_dim = head_dim;
   p.scale_log2 = scale * hcp::kLog2e;
   set_acc(p, acc);
   hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, paged != 0, true,
@@ -357,6 +360,7 @@ int hcp_plan_decode_splits(const hcp_varlen_entry* entries, int32_t num_entries,
 
 size_t hcp_decode_workspace_bytes(int32_t num_splits, int32_t num_heads, int32_t head_dim) {
   if (num_splits <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  head_dim = hcp::padded_head_dim(head_dim);  // partials keep the kernel's width
   const size_t n = static_cast<size_t>(num_splits) * num_heads;
   const size_t o = n * head_dim * sizeof(float);
   const size_t o_al = (o + 255) & ~static_cast<size_t>(255);
@@ -375,8 +379,6 @@ static int decode_impl(const char* who, const void* q, int64_t q_stride_tok,
                        void* stream) {
   int rc = check_heads(num_heads, num_kv_heads, head_dim, dtype, who);
   if (rc) return rc;
-  if (num_heads / num_kv_heads > 16)
-    return fail(HCP_EUNSUPPORTED, "%s: more than 16 query heads per KV head", who);
   if (num_entries < 0 || num_splits < 0 || num_seqs < 0)
     return fail(HCP_EINVAL, "%s: negative counts", who);
   if (num_seqs == 0) return HCP_OK;
@@ -393,7 +395,8 @@ static int decode_impl(const char* who, const void* q, int64_t q_stride_tok,
   if (workspace && !aligned16(workspace))
     return fail(HCP_EINVAL, "%s: workspace not 16-byte aligned", who);
   const size_t n = static_cast<size_t>(num_splits) * num_heads;
-  const size_t o_al = (n * head_dim * sizeof(float) + 255) & ~static_cast<size_t>(255);
+  const size_t o_al = (n * hcp::padded_head_dim(head_dim) * sizeof(float) + 255) &
+                      ~static_cast<size_t>(255);
   hcp::DecParams dp{};
   dp.q = q;
   dp.q_stride_tok = q_stride_tok;
@@ -406,6 +409,8 @@ static int decode_impl(const char* who, const void* q, int64_t q_stride_tok,
   dp.num_heads = num_heads;
   dp.num_kv_heads = num_kv_heads;
   dp.group = num_heads / num_kv_heads;
+  dp.head_chunks = (dp.group + 15) / 16;
+  dp.head_dim = head_dim;
   dp.scale_log2 = scale * hcp::kLog2e;
   hcp::RedParams rp{};
   rp.ws_o = dp.ws_o;
@@ -418,6 +423,7 @@ static int decode_impl(const char* who, const void* q, int64_t q_stride_tok,
   rp.lse = lse;
   rp.lse_stride_head = lse_stride_head;
   rp.num_heads = num_heads;
+  rp.head_dim = head_dim;
   rp.acc_o = acc_o;
   rp.acc_stride_tok = acc_stride_tok;
   rp.acc_stride_head = acc_stride_head;
@@ -591,8 +597,8 @@ int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok, int64_t k_strid
   const char* who = "hcp_reshape_and_cache";
   if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0)
     return fail(HCP_EINVAL, "%s: bad sizes", who);
-  if (head_dim % 8 || (head_dim & (head_dim - 1)))
-    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d must be a power of two >= 8", who, head_dim);
+  if (head_dim % 8)
+    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d must be a multiple of 8", who, head_dim);
   if (!dtype16(dtype)) return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
   if (slot_dtype != HCP_DTYPE_I32 && slot_dtype != HCP_DTYPE_I64)
     return fail(HCP_EUNSUPPORTED, "%s: slot dtype %d (int32 or int64)", who, slot_dtype);
@@ -621,7 +627,8 @@ int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok, int64_t k_strid
   p.slots = slot_mapping;
   p.num_tokens = num_tokens;
   p.num_kv_heads = num_kv_heads;
-  p.cpr_shift = 31 - __builtin_clz(static_cast<unsigned>(head_dim / 8));
+  p.cpr = head_dim / 8;
+  p.cpr_shift = (p.cpr & (p.cpr - 1)) ? -1 : 31 - __builtin_clz(static_cast<unsigned>(p.cpr));
   p.k_cache = reinterpret_cast<void*>(c.k_addr);
   p.v_cache = reinterpret_cast<void*>(c.v_addr);
   p.stride_block = c.stride_block;

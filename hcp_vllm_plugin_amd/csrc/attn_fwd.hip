@@ -107,7 +107,7 @@ __device__ __forceinline__ i16x4 lds_read_tr(const HCP_LDS(char)* p) {
       reinterpret_cast<HCP_LDS(i16x4)*>(const_cast<HCP_LDS(char)*>(p)));
 }
 
-template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN>
+template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN, bool PADDED>
 __global__ __attribute__((amdgpu_flat_work_group_size(kFwdThreads, kFwdThreads),
                           amdgpu_waves_per_eu(HCP_FWD_WAVES_PER_EU, HCP_FWD_WAVES_PER_EU))) void
 fa_fwd_kernel(FwdParams p) {
@@ -184,6 +184,11 @@ fa_fwd_kernel(FwdParams p) {
   const int64_t off = e.causal_offset;
 
   // ---- Q^T fragments (B operand): lane owns query row r32 ----
+  // A row holds dv <= D valid elements (a multiple of 8; PADDED: fewer than
+  // D); the kernel computes in D columns whose tail is zero in Q, K and V
+  // and is never stored.
+  const int dv = PADDED ? p.head_dim : D;
+  const int rowv = dv * 2;  // valid bytes of a row
   const int64_t qi = static_cast<int64_t>(qb) * BM + wave * 32 + r32;
   const bool q_valid = qi < q_len;
   V8 qf[KSTEPS];
@@ -193,7 +198,8 @@ fa_fwd_kernel(FwdParams p) {
                         static_cast<int64_t>(head) * p.q_stride_head) * 2;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-      u32x4 x = q_valid ? ldg16(qrow + (16 * s + 8 * g) * 2) : u32x4{0, 0, 0, 0};
+      u32x4 x = q_valid && 16 * s + 8 * g < dv ? ldg16(qrow + (16 * s + 8 * g) * 2)
+                                               : u32x4{0, 0, 0, 0};
       qf[s] = as_vec8<V8>(x);
     }
   }
@@ -256,11 +262,16 @@ fa_fwd_kernel(FwdParams p) {
   // rows lie in one block -- and offset by the row inside the wave's share.
   constexpr int WROWS = NI * RPI;  // tile rows each wave loads
   static_assert(!PAGED || WROWS <= kFwdPagedMinBlock, "a wave's rows must fit one block");
+  // A chunk past the row's dv elements gets an offset past any num_records:
+  // it reads as zeros.
+  constexpr uint32_t kOob = 0x80000000u;
   uint32_t goff[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
-    goff[i] = static_cast<uint32_t>(PAGED ? lrow(i) - wave * WROWS : lrow(i)) * rowb32 +
-              lchunk(i) * 16u;
+    goff[i] = lchunk(i) * 8 < dv
+                  ? static_cast<uint32_t>(PAGED ? lrow(i) - wave * WROWS : lrow(i)) * rowb32 +
+                        lchunk(i) * 16u
+                  : kOob;
 
   // paged: block ids of the wave's rows, a window of 64 tiles per VGPR (lane
   // l holds the id of tile base + l, clamped to the last tile and to the
@@ -304,7 +315,7 @@ fa_fwd_kernel(FwdParams p) {
     int rows = kv_len - r0;
     rows = rows < WROWS ? rows : WROWS;
     rows = rows < e.kv.block_size - in_blk ? rows : e.kv.block_size - in_blk;
-    const int nrec = rows > 0 ? static_cast<int>((rows - 1) * rowb_g) + ROWB : 0;
+    const int nrec = rows > 0 ? static_cast<int>((rows - 1) * rowb_g) + rowv : 0;
     return __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(seg + static_cast<int64_t>(id) * blockb + in_blk * rowb_g), 0, nrec,
         kBufferRsrcWord3);
@@ -325,7 +336,7 @@ fa_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       uint32_t o = goff[i];
-      if (ragged) {
+      if (ragged && o != kOob) {
         const int key = n0 + lrow(i);
         const int kc = key < kv_len ? key : kv_len - 1;
         o = static_cast<uint32_t>(kc - n0) * rowb32 + lchunk(i) * 16u;
@@ -345,7 +356,7 @@ fa_fwd_kernel(FwdParams p) {
     const int t = tile_idx < ntiles ? tile_idx : ntiles - 1;
     const int rows = kv_len - t * BN;
     const int nrec = rows >= BN ? 0x7fffffff
-                                : static_cast<int>((rows - 1) * rowb_g) + ROWB;
+                                : static_cast<int>((rows - 1) * rowb_g) + rowv;
     return __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(seg + static_cast<int64_t>(t) * BN * rowb_g), 0, nrec,
         kBufferRsrcWord3);
@@ -655,7 +666,7 @@ fa_fwd_kernel(FwdParams p) {
       const __amdgpu_buffer_rsrc_t rk0 = page_rsrc(kseg, id0, 0), rv0 = page_rsrc(vseg, id0, 0);
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const uint32_t o = lrow(i) < lead ? 0x80000000u : goff[i];
+        const uint32_t o = lrow(i) < lead ? kOob : goff[i];
         load_at(rk0, o, i, K0);
         load_at(rv0, o, i, V0);
       }
@@ -710,14 +721,14 @@ fa_fwd_kernel(FwdParams p) {
                         ((e.q_start + wave_q0) * p.acc_stride_tok +
                          static_cast<int64_t>(head) * p.acc_stride_head) * 2;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(abase), 0, static_cast<int>((rows - 1) * sb) + ROWB, kBufferRsrcWord3);
+        const_cast<char*>(abase), 0, static_cast<int>((rows - 1) * sb) + rowv, kBufferRsrcWord3);
 #pragma unroll
     for (int i = 0; i < 32 / RPL; ++i) {
       const int r = i * RPL + lane / CPR;
       const int lc = (lane % CPR) ^ (r & (CPR - 1));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rs, reinterpret_cast<HCP_LDS(void)*>(abuf + i * 1024), 16,
-          static_cast<int>(r * sb) + lc * 16, 0, 0, 0);
+          lc * 8 < dv ? static_cast<int>(r * sb) + lc * 16 : static_cast<int>(kOob), 0, 0, 0);
     }
   }
   if (q_valid) {
@@ -735,7 +746,7 @@ fa_fwd_kernel(FwdParams p) {
           u32x2 w;
           w[0] = pack2<T>(oacc[db][4 * a + 0] * inv, oacc[db][4 * a + 1] * inv);
           w[1] = pack2<T>(oacc[db][4 * a + 2] * inv, oacc[db][4 * a + 3] * inv);
-          *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
+          if (d0 < dv) *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
         }
       }
     } else {
@@ -785,7 +796,7 @@ fa_fwd_kernel(FwdParams p) {
             const float b1 = E::to_float(static_cast<uint16_t>(suf[h] >> 16));
             w[h] = pack2<T>(__builtin_fmaf(a0, ps, b0 * ss), __builtin_fmaf(a1, ps, b1 * ss));
           }
-          *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
+          if (d0 < dv) *reinterpret_cast<u32x2*>(orow + d0 * 2) = w;
         }
       }
     }
@@ -796,25 +807,33 @@ fa_fwd_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 // Host-side launch helpers (called from abi.hip)
 // ---------------------------------------------------------------------------
-template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN>
+template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN, bool PADDED>
 static hipError_t launch_fwd_t(const FwdParams& p, int64_t grid, hipStream_t st) {
-  hipLaunchKernelGGL((fa_fwd_kernel<D, T, CAUSAL, PAGED, VARLEN>),
+  hipLaunchKernelGGL((fa_fwd_kernel<D, T, CAUSAL, PAGED, VARLEN, PADDED>),
                      dim3(static_cast<unsigned>(grid)), dim3(kFwdThreads), 0, st, p);
   return hipGetLastError();
 }
 
-template <int D, typename T>
-static hipError_t launch_fwd_d(const FwdParams& p, int64_t grid, bool causal,
+template <int D, typename T, bool PADDED>
+static hipError_t launch_fwd_p(const FwdParams& p, int64_t grid, bool causal,
                                bool paged, bool varlen, hipStream_t st) {
   if (varlen) {
     if (causal)
-      return paged ? launch_fwd_t<D, T, true, true, true>(p, grid, st)
-                   : launch_fwd_t<D, T, true, false, true>(p, grid, st);
-    return paged ? launch_fwd_t<D, T, false, true, true>(p, grid, st)
-                 : launch_fwd_t<D, T, false, false, true>(p, grid, st);
+      return paged ? launch_fwd_t<D, T, true, true, true, PADDED>(p, grid, st)
+                   : launch_fwd_t<D, T, true, false, true, PADDED>(p, grid, st);
+    return paged ? launch_fwd_t<D, T, false, true, true, PADDED>(p, grid, st)
+                 : launch_fwd_t<D, T, false, false, true, PADDED>(p, grid, st);
   }
-  return causal ? launch_fwd_t<D, T, true, false, false>(p, grid, st)
-                : launch_fwd_t<D, T, false, false, false>(p, grid, st);
+  return causal ? launch_fwd_t<D, T, true, false, false, PADDED>(p, grid, st)
+                : launch_fwd_t<D, T, false, false, false, PADDED>(p, grid, st);
+}
+
+// head_dim == D runs the unpadded instantiations (no per-column checks)
+template <int D, typename T>
+static hipError_t launch_fwd_d(const FwdParams& p, int64_t grid, bool causal,
+                               bool paged, bool varlen, hipStream_t st) {
+  return p.head_dim == D ? launch_fwd_p<D, T, false>(p, grid, causal, paged, varlen, st)
+                         : launch_fwd_p<D, T, true>(p, grid, causal, paged, varlen, st);
 }
 
 hipError_t launch_fwd(const FwdParams& p, int head_dim, int dtype, bool causal,
@@ -822,7 +841,7 @@ hipError_t launch_fwd(const FwdParams& p, int head_dim, int dtype, bool causal,
   const int64_t grid =
       xcd_grid_size(static_cast<int64_t>(p.num_tiles) * p.group, p.num_kv_heads);
   if (grid <= 0) return hipSuccess;
-  if (head_dim == 128) {
+  if (head_dim > 64) {  // 72 .. 128: computed in 128 columns, the tail zero
     return dtype == HCP_DTYPE_BF16
                ? launch_fwd_d<128, __bf16>(p, grid, causal, paged, varlen, st)
                : launch_fwd_d<128, _Float16>(p, grid, causal, paged, varlen, st);

@@ -11,8 +11,9 @@
 // skipped as well, so a bad mapping cannot write outside the cache.
 //
 // HBM-bound copy: each thread moves 16 bytes (8 elements) of one (token,
-// head) row of K and of V, so a wave covers whole 256-byte rows (D = 128) on
-// both sides: 2 * n * Hkv * D * 2 bytes read and the same written.
+// head) row of K and of V, so a wave covers whole rows (four 256-byte rows
+// at D = 128) on both sides: 2 * n * Hkv * D * 2 bytes read and the same
+// written.  Any head_dim that is a multiple of 8.
 #include "params.h"
 
 namespace hcp {
@@ -20,9 +21,11 @@ namespace hcp {
 template <typename SlotT>
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(CacheParams p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t row = gid >> p.cpr_shift;  // (token, head) row
+  // (token, head) row and 16-byte chunk: a shift for a power-of-two chunk
+  // count, else a division (workgroup-uniform choice)
+  const int64_t row = p.cpr_shift >= 0 ? gid >> p.cpr_shift : gid / p.cpr;
   if (row >= p.num_tokens * p.num_kv_heads) return;
-  const int ch = static_cast<int>(gid & ((1 << p.cpr_shift) - 1));
+  const int ch = static_cast<int>(gid - row * p.cpr);
   const int64_t t = row / p.num_kv_heads;
   const int h = static_cast<int>(row - t * p.num_kv_heads);
   const int64_t slot = static_cast<int64_t>(reinterpret_cast<const SlotT*>(p.slots)[t]);
@@ -42,7 +45,7 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(CacheParams p) {
 }
 
 hipError_t launch_cache_write(const CacheParams& p, bool slots_i64, hipStream_t st) {
-  const int64_t threads = (p.num_tokens * p.num_kv_heads) << p.cpr_shift;
+  const int64_t threads = p.num_tokens * p.num_kv_heads * p.cpr;
   const int64_t grid = (threads + 255) / 256;
   if (grid <= 0) return hipSuccess;
   if (slots_i64)

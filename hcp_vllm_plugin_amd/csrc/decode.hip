@@ -5,11 +5,13 @@
 // workgroups on a 256-CU part, 63 of 64 query rows padding, and every query
 // head of a GQA group re-reading the same K/V.  Here:
 //
-//  * kernel 1 (decode_split_kernel): one workgroup per (split, KV head).  A
-//    split is a key range of one segment (contiguous peer or paged local; the
-//    form is per entry, so one launch serves both).  All G query
-//    heads of the KV head are the 16 columns of v_mfma_f32_16x16x32 (G <= 16),
-//    so each K/V byte is read from HBM once.  Each of the 4 waves walks its
+//  * kernel 1 (decode_split_kernel): one workgroup per (split, KV head,
+//    head chunk).  A split is a key range of one segment (contiguous peer or
+//    paged local; the form is per entry, so one launch serves both).  Up to 16
+//    query heads of the KV head are the 16 columns of v_mfma_f32_16x16x32, so
+//    with G <= 16 each K/V byte is read from HBM once; a larger group runs in
+//    ceil(G / 16) chunks of 16 heads, dispatched next to each other so the
+//    chunks after the first mostly read the split's K/V from L2.  Each of the 4 waves walks its
 //    own 32-key chunks straight from global memory into MFMA operands (no LDS,
 //    no barrier in the loop); the next chunk's loads are in flight while the
 //    current one is computed.
@@ -46,7 +48,8 @@ struct DecShared {
 };
 
 template <int D, typename T, bool PAGED>
-__device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in, int sp,
+__device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in, int chunk_in,
+                                                  int sp,
                                                   const hcp_varlen_entry& e,
                                                   const hcp_decode_split& spl,
                                                   char (*bufE)[2 * DecShared<D>::CHB],
@@ -73,25 +76,35 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
-  const int G = p.group;
-  // the KV head is workgroup-uniform: keep every address built from it in
-  // SGPRs (buffer descriptors from VGPR values become waterfall loops)
+  // the KV head and head chunk are workgroup-uniform: keep every address
+  // built from them in SGPRs (buffer descriptors from VGPR values become
+  // waterfall loops).  This workgroup's query heads: h0 .. h0 + G - 1.
   const int kvh = __builtin_amdgcn_readfirstlane(kvh_in);
+  const int chunk = __builtin_amdgcn_readfirstlane(chunk_in);
+  const int G = p.group - 16 * chunk < 16 ? p.group - 16 * chunk : 16;
+  const int h0 = kvh * p.group + 16 * chunk;
   KvAddr kva;
   kva.init(e.kv);
   const int64_t kb = spl.key_begin, ke = spl.key_end;
 
-  // Q^T (B operand): column c16 = query head kvh*G + c16 (zero for c16 >= G);
+  // A row holds dv <= D valid elements (a multiple of 8): the kernel computes
+  // in D columns.  Q's tail is zero; a K/V chunk past dv is fetched from the
+  // row's first chunk instead (finite values that meet Q's zero columns, or
+  // land in output columns that are never stored), so no load leaves the row.
+  const int dv = p.head_dim;
+  const int cv = dv / 8;  // valid 16-byte chunks of a row
+  // Q^T (B operand): column c16 = query head h0 + c16 (zero for c16 >= G);
   // k-step s covers d = 32s .. 32s+31 (lane group g4: 8 of them)
   V8 qf[QSTEPS];
   {
     const bool hv = c16 < G;
     const char* qrow = reinterpret_cast<const char*>(p.q) +
                        (e.q_start * p.q_stride_tok +
-                        static_cast<int64_t>(kvh * G + (hv ? c16 : 0)) * p.q_stride_head) * 2;
+                        static_cast<int64_t>(h0 + (hv ? c16 : 0)) * p.q_stride_head) * 2;
 #pragma unroll
     for (int s = 0; s < QSTEPS; ++s) {
-      u32x4 x = hv ? ldg16(qrow + (32 * s + 8 * g4) * 2) : u32x4{0, 0, 0, 0};
+      u32x4 x = hv && 32 * s + 8 * g4 < dv ? ldg16(qrow + (32 * s + 8 * g4) * 2)
+                                           : u32x4{0, 0, 0, 0};
       qf[s] = as_vec8<V8>(x);
     }
   }
@@ -113,7 +126,7 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
     if constexpr (!PAGED) {
       const int64_t rows = ke - k0;  // >= 1 valid rows in this chunk
       const int nrec = rows >= kDecChunk ? 0x7fffffff
-                                         : static_cast<int>((rows - 1) * rowb_g) + ROWB;
+                                         : static_cast<int>((rows - 1) * rowb_g) + 2 * dv;
       const int64_t base = ((kva.start + k0) * kva.stride_tok +
                             static_cast<int64_t>(kvh) * kva.stride_head) * 2;
       const __amdgpu_buffer_rsrc_t rk =
@@ -123,7 +136,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         const int row = j * KPI + kr;
-        const int off = static_cast<int>(row * rowb_g) + 16 * (sl ^ (row % CPR));
+        int ch = sl ^ (row % CPR);
+        ch = ch < cv ? ch : 0;
+        const int off = static_cast<int>(row * rowb_g) + 16 * ch;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rk, reinterpret_cast<HCP_LDS_PTR(void)>(dst + j * 1024), 16, off, 0, 0, kStreamAux);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -274,7 +289,9 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
           int64_t key = k0 + row;
           key = key < ke ? key : ke - 1;
           const int64_t x = kva.start + key;
-          const int64_t inb = (x & kva.bs_mask) * rowb_g + 16 * (sl ^ (row % CPR));
+          int ch = sl ^ (row % CPR);
+          ch = ch < cv ? ch : 0;
+          const int64_t inb = (x & kva.bs_mask) * rowb_g + 16 * ch;
           if constexpr (decltype(buf)::value) {
             const uint32_t off = ids[j] * static_cast<uint32_t>(blockb) + static_cast<uint32_t>(inb);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -373,7 +390,7 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
       L += sm_l[w][h] * sc;
       O += sm_o[w][h][d] * sc;
     }
-    const int head = kvh * G + h;
+    const int head = h0 + h;
     const int64_t slot = static_cast<int64_t>(sp) * p.num_heads + head;
     p.ws_o[slot * D + d] = L > 0.f ? O / L : 0.f;
     if (d == 0) p.ws_lse[slot] = L > 0.f ? M * kLn2 + __logf(L) : -INFINITY;
@@ -393,14 +410,17 @@ decode_split_kernel(DecParams p) {
   __shared__ float sm_l[4][16];
   int kvh;
   int64_t item;
-  if (!xcd_remap(blockIdx.x, p.num_splits, p.num_kv_heads, &kvh, &item)) return;
-  const hcp_decode_split spl = p.splits[item];
+  if (!xcd_remap(blockIdx.x, static_cast<int64_t>(p.num_splits) * p.head_chunks,
+                 p.num_kv_heads, &kvh, &item))
+    return;
+  const int chunk = static_cast<int>(item % p.head_chunks);
+  const hcp_decode_split spl = p.splits[item / p.head_chunks];
   const int sp = spl.slot;  // workspace partial of this split
   const hcp_varlen_entry e = p.entries[spl.entry];
   if (e.kv.block_table != 0)
-    decode_split_body<D, T, true>(p, kvh, sp, e, spl, bufE, bufO, sm_m, sm_l);
+    decode_split_body<D, T, true>(p, kvh, chunk, sp, e, spl, bufE, bufO, sm_m, sm_l);
   else
-    decode_split_body<D, T, false>(p, kvh, sp, e, spl, bufE, bufO, sm_m, sm_l);
+    decode_split_body<D, T, false>(p, kvh, chunk, sp, e, spl, bufE, bufO, sm_m, sm_l);
 }
 
 // Merge every partial of one (sequence, query head) -- and the running
@@ -431,7 +451,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
     if (acc_l == INFINITY) acc_l = -INFINITY;  // merge_attn_states reads +inf as empty
     const uint16_t* arow = reinterpret_cast<const uint16_t*>(p.acc_o) +
                            seq * p.acc_stride_tok + static_cast<int64_t>(head) * p.acc_stride_head;
-    acc_v = Elem<T>::to_float(arow[d]);
+    acc_v = d < p.head_dim ? Elem<T>::to_float(arow[d]) : 0.f;
   }
 
   float m = -INFINITY;
@@ -477,14 +497,15 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
   }
   uint16_t* orow = reinterpret_cast<uint16_t*>(p.out) + seq * p.o_stride_tok +
                    static_cast<int64_t>(head) * p.o_stride_head;
-  orow[d] = Elem<T>::from_float(o);
+  if (d < p.head_dim) orow[d] = Elem<T>::from_float(o);
   if (p.lse != nullptr && d == 0)
     p.lse[static_cast<int64_t>(head) * p.lse_stride_head + seq] = lse;
 }
 
 template <int D, typename T>
 static hipError_t launch_dec_t(const DecParams& dp, const RedParams& rp, hipStream_t st) {
-  const int64_t grid = xcd_grid_size(dp.num_splits, dp.num_kv_heads);
+  const int64_t grid =
+      xcd_grid_size(static_cast<int64_t>(dp.num_splits) * dp.head_chunks, dp.num_kv_heads);
   if (grid > 0) {
     hipLaunchKernelGGL((decode_split_kernel<D, T>), dim3(static_cast<unsigned>(grid)),
                        dim3(kDecThreads), 0, st, dp);
@@ -502,7 +523,7 @@ static hipError_t launch_dec_t(const DecParams& dp, const RedParams& rp, hipStre
 
 hipError_t launch_decode(const DecParams& dp, const RedParams& rp, int head_dim,
                          int dtype, hipStream_t st) {
-  if (head_dim == 128)
+  if (head_dim > 64)  // 72 .. 128: computed in 128 columns
     return dtype == HCP_DTYPE_BF16 ? launch_dec_t<128, __bf16>(dp, rp, st)
                                    : launch_dec_t<128, _Float16>(dp, rp, st);
   return dtype == HCP_DTYPE_BF16 ? launch_dec_t<64, __bf16>(dp, rp, st)

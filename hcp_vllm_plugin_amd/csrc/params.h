@@ -14,6 +14,10 @@ constexpr int kFwdBM = 32 * HCP_FWD_WAVES;  // query rows per prefill workgroup
 constexpr int kFwdBN = 64;                  // keys per prefill tile
 constexpr int kFwdPagedMinBlock = 16;      // paged prefill: rows a wave reads from one block
 
+// Column width the attention kernels compute a head_dim in: 64 or 128 (a
+// smaller head_dim, a multiple of 8, is zero-padded to it inside the kernels).
+__host__ __device__ constexpr int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : 128; }
+
 struct FwdParams {
   const void* q;
   int64_t q_stride_tok, q_stride_head;
@@ -25,6 +29,7 @@ struct FwdParams {
   const int32_t* tiles;             // varlen: device (entry, q_block) pairs
   int32_t num_tiles;                // varlen: tiles; else query blocks
   int32_t num_heads, num_kv_heads, group;
+  int32_t head_dim;  // valid elements per row (<= the kernel's width; the tail is padding)
   float scale_log2;
   int32_t window;           // causal only: key j visible iff j > qpos - window (0: none)
   hcp_varlen_entry single;  // non-varlen: the one entry
@@ -47,6 +52,8 @@ struct DecParams {
   float* ws_o;    // [num_splits, H, D]
   float* ws_lse;  // [num_splits, H]
   int32_t num_heads, num_kv_heads, group;
+  int32_t head_chunks;  // ceil(group / 16): workgroups per (split, KV head)
+  int32_t head_dim;     // valid elements per row (<= the kernel's width)
   float scale_log2;
 };
 
@@ -60,6 +67,7 @@ struct RedParams {
   float* lse;
   int64_t lse_stride_head;
   int32_t num_heads;
+  int32_t head_dim;  // valid elements per row (<= the kernel's width)
   // optional running accumulator merged in as one more partial (NULL: none)
   const void* acc_o;
   int64_t acc_stride_tok, acc_stride_head;
@@ -93,7 +101,8 @@ struct CacheParams {
   const void* slots;  // int32 or int64, one per token
   int64_t num_tokens;
   int32_t num_kv_heads;
-  int32_t cpr_shift;  // log2(head_dim / 8): 16-byte chunks per row
+  int32_t cpr;        // head_dim / 8: 16-byte chunks per row
+  int32_t cpr_shift;  // log2(cpr) when cpr is a power of two, else -1
   void* k_cache;
   void* v_cache;
   int64_t stride_block, stride_head, stride_tok;

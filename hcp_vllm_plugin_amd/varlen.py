@@ -411,6 +411,12 @@ def head_major(t: torch.Tensor) -> torch.Tensor:
     return t.permute(1, 0, 2).contiguous().permute(1, 0, 2)
 
 
+def head_chunks(num_heads: int, num_kv_heads: int) -> int:
+    """Decode workgroups per (split, KV head): the split kernel takes up to 16
+    query heads of a KV group at a time."""
+    return -(-(num_heads // num_kv_heads) // 16)
+
+
 def choose_split_tokens(seg_lens: list[int], num_kv_heads: int, num_cus: int = 256,
                         max_rounds: int = 4, round_keys: int = 2048, minimum: int = 64,
                         maximum: int = 16384) -> int:
@@ -455,7 +461,8 @@ class DecodeBatch:
         self.num_seqs = len(segments)
         self.num_entries = len(entries)
         if split_tokens is None:
-            split_tokens = choose_split_tokens([e.kv.len for e in entries], num_kv_heads)
+            split_tokens = choose_split_tokens([e.kv.len for e in entries],
+                                               num_kv_heads * head_chunks(num_heads, num_kv_heads))
         self.split_tokens = split_tokens
         arr = (VarlenEntry * max(self.num_entries, 1))(*entries)
         seq_arr = (ctypes.c_int32 * max(self.num_entries, 1))(*seq_of)
@@ -507,7 +514,8 @@ class DecodeBatch:
         self.num_entries = n
         lens = entries["len"]
         if split_tokens is None:
-            split_tokens = choose_split_tokens([int(lens.sum())], num_kv_heads)
+            split_tokens = choose_split_tokens([int(lens.sum())],
+                                               num_kv_heads * head_chunks(num_heads, num_kv_heads))
         self.split_tokens = split_tokens
         arr = entries if n else np.zeros(1, dtype=ENTRY_DTYPE)
         cap = int(((lens + split_tokens - 1) // split_tokens).sum())

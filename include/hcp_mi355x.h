@@ -41,7 +41,7 @@ extern "C" {
 typedef enum hcp_status {
   HCP_OK = 0,
   HCP_EINVAL = -1,       /* bad argument: null pointer, negative size, H % Hkv != 0, ... */
-  HCP_EUNSUPPORTED = -2, /* valid but not built: head_dim not 64/128, dtype, ... */
+  HCP_EUNSUPPORTED = -2, /* valid but not built: head_dim not a multiple of 8 up to 128, dtype, ... */
   HCP_ELAUNCH = -3,      /* the HIP runtime rejected a launch */
   HCP_EWORKSPACE = -4    /* caller workspace smaller than required */
 } hcp_status;
@@ -125,7 +125,11 @@ const char* hcp_last_error(void);
  * position p = causal_offset + i sees keys j with p - window < j <= p; the
  * reference's Triton path has no window and falls back to torch for it
  * (:315-323).  window = 0: none.
- * dtype: HCP_DTYPE_F16 or HCP_DTYPE_BF16 for q/k/v/out.  head_dim 64 or 128.
+ * dtype: HCP_DTYPE_F16 or HCP_DTYPE_BF16 for q/k/v/out.  head_dim: any
+ * multiple of 8 up to 128 (the reference takes any head_dim, padding it to a
+ * power of two with masked columns, ring_triton_attn.py:69-78,201; here the
+ * kernels compute in 64 or 128 columns whose tail they load as zeros and
+ * never store).  The same holds for every attention entry point below.
  */
 int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
                      float* lse, int64_t tq, int64_t tk, int32_t num_heads,
@@ -249,7 +253,8 @@ int hcp_plan_decode_splits(const hcp_varlen_entry* entries,
                            int32_t split_tokens, hcp_decode_split* splits_out,
                            int32_t cap, int32_t* seq_partial_start);
 
-/* Bytes of workspace hcp_decode_splitkv needs for `num_splits` partials. */
+/* Bytes of workspace hcp_decode_splitkv needs for `num_splits` partials
+ * (kept at the kernel's 64- or 128-column width). */
 size_t hcp_decode_workspace_bytes(int32_t num_splits, int32_t num_heads,
                                   int32_t head_dim);
 
@@ -258,8 +263,10 @@ size_t hcp_decode_workspace_bytes(int32_t num_splits, int32_t num_heads,
  * per-request local pass, peer pass and merge of HcpRingAttentionImpl.forward
  * (ring_backend.py:611-832 with tq == 1; the local segment of the decode
  * branch :663-679) that launch the flash kernel with grid (H, 1).  Kernel 1
- * computes one fp32 (O, LSE) partial per split and KV head, all G query heads
- * of a KV group together so K/V are read once.  Kernel 2 merges every partial
+ * computes one fp32 (O, LSE) partial per split and query head, up to 16 query
+ * heads of a KV group in one workgroup so K/V are read once (any group size:
+ * a larger group runs in chunks of 16 heads, the reference's any-G head map
+ * h / G of ring_triton_attn.py:64).  Kernel 2 merges every partial
  * of a sequence -- all splits of its local and peer segments -- into `out`
  * (dtype) and, when `lse` is not NULL, the merged LSE [H, num_seqs]
  * (ring_decode.py:46-61 semantics).  Output row of sequence s is row s.

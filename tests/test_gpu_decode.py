@@ -72,6 +72,20 @@ def test_decode_fp16_d64(dev):
           bs=16, seed=53, split=128)
 
 
+@pytest.mark.parametrize("h,hkv,d,dtype", [
+    (32, 1, 128, torch.bfloat16),   # MQA: G = 32, two full head chunks
+    (28, 1, 128, torch.bfloat16),   # G = 28: chunks of 16 and 12 heads
+    (40, 2, 64, torch.float16),     # G = 20
+    (17, 1, 64, torch.bfloat16),    # G = 17: a 1-head second chunk
+])
+@pytest.mark.parametrize("split", [None, 64])
+def test_decode_groups_above_16(dev, h, hkv, d, dtype, split):
+    """Query-head groups larger than the 16 MFMA columns (any G, as the
+    reference's head map h / G, ring_triton_attn.py:64)."""
+    _case(dev, h, hkv, d, dtype, peer_lens=[1500, 0, 64], loc_lens=[300, 800, 1],
+          bs=16, seed=54 + h + hkv, split=split)
+
+
 @pytest.mark.parametrize("split", [None, 16, 64])
 def test_decode_paged_cache_past_4gib_nan_outside_segments(dev, split):
     """A cache of 4.6 GB (its span from a head's base exceeds 4 GiB, so the

@@ -1,0 +1,174 @@
+"""GPU parity at head_dims other than 64 / 128.
+
+The reference kernel takes any head_dim (BLOCK_D = next power of two with the
+columns past head_dim masked, ring_triton_attn.py:69-78,201).  The HIP
+kernels compute in 64 or 128 columns and treat the tail as zeros: every entry
+point is checked here against the oracle at head_dims that are multiples of 8
+below 128 -- the plain and merging forward passes, the paged varlen pass, the
+split-KV decode, the paged KV write and the backend's forward.  Rows are
+packed at their true width ([T, H, head_dim], stride head_dim), so a load
+past a row's end would read the neighbouring head or token and show.
+"""
+
+import types
+
+import pytest
+import torch
+
+from hcp_vllm_plugin_amd import merge_attn_states, ring_attn_merged, ring_attn_with_lse
+from hcp_vllm_plugin_amd import ring_backend as rb
+from hcp_vllm_plugin_amd.kv_cache import reshape_and_cache
+from hcp_vllm_plugin_amd.varlen import (
+    PagedCache, make_entry, segment_contiguous, segment_paged, varlen_attn_with_lse)
+from oracle import ring_oracle as orc
+from tests._util import LSE_TOL, OUT_TOL, max_err, outlier_k, randn, scale_for
+from tests.test_gpu_decode import _case as decode_case
+from tests.test_gpu_kv_cache import _case as cache_case
+from tests.test_gpu_varlen import _build as varlen_build
+
+pytestmark = pytest.mark.gpu
+
+DIMS = [8, 40, 72, 80, 96, 112]
+
+
+@pytest.mark.parametrize("d", DIMS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("off", [None, 400, -30])
+def test_forward_head_dims(dev, d, dtype, off):
+    gen = torch.Generator().manual_seed(d + (off or 0))
+    tq, tk, h, hkv = 300, 700, 14, 2
+    q = randn(gen, (tq, h, d), dtype)
+    k = outlier_k(randn(gen, (tk, hkv, d), dtype), gen, n_channels=min(4, d)).to(dtype)
+    v = randn(gen, (tk, hkv, d), dtype)
+    scale = scale_for(d)
+    o, lse = ring_attn_with_lse(q.to(dev), k.to(dev), v.to(dev), scale, off)
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_with_lse(q.float(), k.float(), v.float(), scale, off)
+    assert o.shape == (tq, h, d)
+    assert max_err(o, ro) <= OUT_TOL[dtype], max_err(o, ro)
+    assert max_err(lse, rl) <= LSE_TOL
+
+
+@pytest.mark.parametrize("d", [40, 96])
+def test_merged_pass_head_dims(dev, d):
+    """Local pass merging a peer partial (the acc epilogue) equals pass +
+    merge_attn_states bit for bit, and the oracle's merge within tolerance."""
+    gen = torch.Generator().manual_seed(70 + d)
+    tq, h, hkv, dtype = 260, 28, 4, torch.bfloat16
+    q = randn(gen, (tq, h, d), dtype).to(dev)
+    kl, vl = (randn(gen, (tq, hkv, d), dtype).to(dev) for _ in range(2))
+    kp, vp = (randn(gen, (333, hkv, d), dtype).to(dev) for _ in range(2))
+    scale = scale_for(d)
+    o_p, l_p = ring_attn_with_lse(q, kp, vp, scale, None)
+    o_l, l_l = ring_attn_with_lse(q, kl, vl, scale, 0)
+    ref = torch.empty_like(q)
+    merge_attn_states(ref, o_p, l_p, o_l, l_l)
+    lse = torch.empty_like(l_p)
+    out = ring_attn_merged(q, kl, vl, scale, 0, o_p, l_p, output_lse=lse)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    rl, rll = orc.attn_with_lse(q.float().cpu(), kl.float().cpu(), vl.float().cpu(), scale, 0)
+    rp, rpl = orc.attn_with_lse(q.float().cpu(), kp.float().cpu(), vp.float().cpu(), scale, None)
+    assert max_err(out, orc.lse_merge(rl, rll, rp, rpl)) <= OUT_TOL[dtype]
+
+
+@pytest.mark.parametrize("layout", ["v031", "v023"])
+@pytest.mark.parametrize("d", [80, 40])
+def test_varlen_paged_head_dims(dev, layout, d):
+    h, hkv, bs, dtype = 28, 4, 16, torch.bfloat16
+    lens, peers = [300, 1, 129, 64], [512, 48, 0, 32]
+    cache, bt, q, peer = varlen_build(dev, layout, lens, peers, h, hkv, d, dtype, bs, seed=42)
+    cd, btd, qd, pd = cache.to(dev), bt.to(dev), q.to(dev), peer.to(dev)
+    pc = PagedCache.from_tensor(cd)
+    pk, pv = pd[:, 0], pd[:, 1]
+    loc_e, peer_e = [], []
+    qs = ps = 0
+    for r, (L, P) in enumerate(zip(lens, peers)):
+        loc_e.append(make_entry(qs, L, segment_paged(pc, btd[r], P, L), 0))
+        peer_e.append(make_entry(qs, L, segment_contiguous(pk, pv, ps, P), 0))
+        qs += L
+        ps += P
+    scale = scale_for(d)
+    o_loc, lse_loc = varlen_attn_with_lse(qd, loc_e, True, hkv, scale)
+    o_peer, lse_peer = varlen_attn_with_lse(qd, peer_e, False, hkv, scale)
+    torch.cuda.synchronize()
+    qs = ps = 0
+    for r, (L, P) in enumerate(zip(lens, peers)):
+        qr = q[qs:qs + L].float()
+        kl, vl = orc.gather_paged(cache.float(), bt[r], P, L, layout)
+        rl, rll = orc.attn_with_lse(qr, kl, vl, scale, 0)
+        rp, rpl = orc.attn_with_lse(qr, peer[ps:ps + P, 0].float(), peer[ps:ps + P, 1].float(),
+                                    scale, None)
+        sl = slice(qs, qs + L)
+        assert max_err(o_loc[sl], rl) <= OUT_TOL[dtype], r
+        assert max_err(lse_loc[:, sl], rll) <= LSE_TOL, r
+        assert max_err(o_peer[sl], rp) <= OUT_TOL[dtype], r
+        assert max_err(lse_peer[:, sl], rpl) <= LSE_TOL, r
+        qs += L
+        ps += P
+
+
+@pytest.mark.parametrize("h,hkv,d,dtype", [(28, 4, 96, torch.bfloat16),
+                                          (14, 2, 80, torch.float16),
+                                          (32, 1, 40, torch.bfloat16)])
+@pytest.mark.parametrize("split", [None, 64])
+def test_decode_head_dims(dev, h, hkv, d, dtype, split):
+    decode_case(dev, h, hkv, d, dtype, peer_lens=[1500, 0, 64], loc_lens=[300, 800, 1],
+                bs=16, seed=80 + d, split=split)
+
+
+@pytest.mark.parametrize("layout", ["v031", "v023"])
+@pytest.mark.parametrize("d", [96, 40, 200])
+def test_cache_write_head_dims(dev, layout, d):
+    cache, key, value, slots = cache_case(layout, torch.bfloat16, torch.int64, 333, 41, 16, 4,
+                                          d, 90 + d)
+    ref = cache.clone()
+    orc.kv_cache_update(key, value, ref, slots, layout)
+    dcache = cache.to(dev)
+    reshape_and_cache(key.to(dev), value.to(dev), dcache, slots.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(dcache.cpu(), ref)
+
+
+@pytest.mark.parametrize("d", [96, 80])
+def test_backend_forward_head_dims(dev, d):
+    """HcpRingAttentionImpl.forward at head_size d: prefill rows (with a
+    staged peer chunk) and a decode row, paged cache [nb, Hkv, 16, 2d]."""
+    rb.clear_peer_kv()
+    gen = torch.Generator().manual_seed(100 + d)
+    h, hkv, bs, dtype = 28, 4, 16, torch.bfloat16
+    reqs = [(200, 200 + 64), (1, 700), (77, 77)]
+    seq_lens = [tk for _, tk in reqs]
+    qsl = [0]
+    for tq, _ in reqs:
+        qsl.append(qsl[-1] + tq)
+    nb = sum(-(-tk // bs) for tk in seq_lens) + 4
+    cache = randn(gen, (nb, hkv, bs, 2 * d), dtype)
+    blocks = [-(-tk // bs) for tk in seq_lens]
+    perm = torch.randperm(nb, generator=gen).to(torch.int32)
+    bt = torch.zeros(len(reqs), max(blocks) + 1, dtype=torch.int32)
+    o = 0
+    for r, n in enumerate(blocks):
+        bt[r, :n] = perm[o:o + n]
+        o += n
+    query = randn(gen, (qsl[-1], h, d), dtype)
+    layer = types.SimpleNamespace(layer_name="model.layers.0.self_attn.attn")
+    kp, vp = randn(gen, (96, hkv, d), dtype), randn(gen, (96, hkv, d), dtype)
+    rb.stage_peer_kv("c0", layer.layer_name, kp.to(dev), vp.to(dev))
+    rb.map_request_peer(int(bt[0, 0]), ["c0"])
+    impl = rb.HcpRingAttentionImpl(h, d, scale_for(d), hkv)
+    meta = types.SimpleNamespace(
+        num_actual_tokens=qsl[-1],
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32, device=dev),
+        seq_lens=torch.tensor(seq_lens, dtype=torch.int32, device=dev),
+        block_table=bt.to(dev))
+    out = torch.empty(qsl[-1], h, d, dtype=dtype, device=dev)
+    try:
+        impl.forward(layer, query.to(dev), None, None, cache.to(dev), meta, out)
+        torch.cuda.synchronize()
+    finally:
+        rb.clear_peer_kv()
+    ref = orc.ring_forward(query.float(), cache.float(), "v031", qsl, seq_lens, bt, scale_for(d),
+                           peers=[(kp.float(), vp.float()), None, None],
+                           out_dtype=torch.float32)
+    assert max_err(out, ref) <= OUT_TOL[dtype]
