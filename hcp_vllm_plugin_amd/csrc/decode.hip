@@ -425,17 +425,23 @@ decode_split_kernel(DecParams p) {
 
 // Merge every partial of one (sequence, query head) -- and the running
 // accumulator, when given -- into the output row and its LSE.  One workgroup
-// of D threads per (sequence, head), thread d owns column d.  The max over
+// of D threads per (sequence, head) column group, thread d owns column d;
+// with many partials per sequence (1, 2 or 4 groups) the groups take
+// interleaved shares of the partials and are summed through LDS.  The max over
 // partial LSEs is thread-strided plus a block reduction; the weighted sum
 // issues 8 partials' loads before consuming them, so a long sequence (one
 // request split over the whole machine) is not a chain of dependent loads.
 template <int D, typename T>
-__global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
-  constexpr int kWaves = D / 64;
-  __shared__ float sm_max[kWaves];
+__global__ __launch_bounds__(4 * D) void decode_reduce_kernel(RedParams p) {
+  constexpr int kMaxWaves = 4 * D / 64;
+  __shared__ float sm_max[kMaxWaves];
+  __shared__ float sm_s[4];
+  __shared__ float sm_o[4][D];
+  const int ng = p.groups;  // column groups; group gi takes partials gi, gi + ng, ...
   const int sh = blockIdx.x;
   const int seq = sh / p.num_heads, head = sh % p.num_heads;
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int d = tid % D, gi = tid / D;
   const int p0 = p.seq_partial_start[seq], p1 = p.seq_partial_start[seq + 1];
   const int n = p1 - p0;
   const int64_t lstep = p.num_heads;
@@ -444,7 +450,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
   const float* ocol = p.ws_o + (static_cast<int64_t>(p0) * lstep + head) * D + d;
 
   // accumulator first: out / lse may alias acc_o / acc_lse, and every read
-  // of them happens before the barrier below, every write after it
+  // of them happens before the barriers below, every write after them
   float acc_l = -INFINITY, acc_v = 0.f;
   if (p.acc_lse != nullptr) {
     acc_l = p.acc_lse[static_cast<int64_t>(head) * p.acc_lse_stride_head + seq];
@@ -454,26 +460,27 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
     acc_v = d < p.head_dim ? Elem<T>::to_float(arow[d]) : 0.f;
   }
 
+  // max over the partial LSEs, thread-strided over the whole block
   float m = -INFINITY;
-  for (int i = d; i < n; i += D) m = fmaxf(m, lcol[i * lstep]);
+  for (int i = tid; i < n; i += ng * D) m = fmaxf(m, lcol[i * lstep]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if ((d & 63) == 0) sm_max[d >> 6] = m;
+  if ((tid & 63) == 0) sm_max[tid >> 6] = m;
   __syncthreads();
   float M = acc_l;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_max[w]);
+  for (int w = 0; w < ng * D / 64; ++w) M = fmaxf(M, sm_max[w]);
 
-  float o = 0.f, lse = -INFINITY;
+  // this group's share of the weighted sum (S is the same in every column
+  // of the group); 8 partials' loads are issued before they are consumed
+  float S = 0.f, O = 0.f;
   if (M != -INFINITY) {
-    float S = 0.f, O = 0.f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
+    int i = gi;
+    for (; i + 7 * ng < n; i += 8 * ng) {
       float l[8], v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        l[j] = lcol[(i + j) * lstep];
-        v[j] = ocol[(i + j) * ostep];
+        l[j] = lcol[(i + j * ng) * lstep];
+        v[j] = ocol[(i + j * ng) * ostep];
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -482,11 +489,24 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(RedParams p) {
         O += w * v[j];
       }
     }
-    for (; i < n; ++i) {
+    for (; i < n; i += ng) {
       const float w = __expf(lcol[i * lstep] - M);
       S += w;
       O += w * ocol[i * ostep];
     }
+  }
+  if (ng > 1) {
+    if (d == 0) sm_s[gi] = S;
+    sm_o[gi][d] = O;
+    __syncthreads();
+    if (gi != 0) return;
+    for (int g2 = 1; g2 < ng; ++g2) {
+      S += sm_s[g2];
+      O += sm_o[g2][d];
+    }
+  }
+  float o = 0.f, lse = -INFINITY;
+  if (M != -INFINITY) {
     if (acc_l != -INFINITY) {
       const float w = __expf(acc_l - M);
       S += w;
@@ -514,8 +534,13 @@ static hipError_t launch_dec_t(const DecParams& dp, const RedParams& rp, hipStre
   }
   const int64_t rgrid = static_cast<int64_t>(rp.num_seqs) * rp.num_heads;
   if (rgrid > 0) {
+    // more column groups when a sequence has many partials (one long
+    // request split over the whole machine): shorter dependent load chains
+    RedParams r = rp;
+    const int per_seq = rp.num_seqs > 0 ? dp.num_splits / rp.num_seqs : 0;
+    r.groups = per_seq >= 48 ? 4 : per_seq >= 24 ? 2 : 1;
     hipLaunchKernelGGL((decode_reduce_kernel<D, T>), dim3(static_cast<unsigned>(rgrid)),
-                       dim3(D), 0, st, rp);
+                       dim3(D * r.groups), 0, st, r);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -68,6 +68,7 @@ struct RedParams {
   int64_t lse_stride_head;
   int32_t num_heads;
   int32_t head_dim;  // valid elements per row (<= the kernel's width)
+  int32_t groups;    // 1, 2 or 4 column groups per (sequence, head), each over a share of the partials
   // optional running accumulator merged in as one more partial (NULL: none)
   const void* acc_o;
   int64_t acc_stride_tok, acc_stride_head;

@@ -17,7 +17,21 @@ import torch
 
 from . import _lib
 
-__all__ = ["ring_attn_with_lse", "ring_attn_merged", "check_qkv"]
+__all__ = ["ring_attn_with_lse", "ring_attn_merged", "check_qkv", "COPY_STATS"]
+
+# Layout copies made on the way into the kernels: an input whose layout the
+# kernel cannot load directly (rows not 16-byte aligned, strides not
+# multiples of 8 elements, k and v with different strides) is copied
+# contiguous first, as the reference's dispatch copies every input
+# (ring_backend.py:328).  Counted here so the extra HBM traffic is visible.
+COPY_STATS: dict = {"tensors": 0, "bytes": 0}
+
+
+def _copied(t: torch.Tensor) -> torch.Tensor:
+    c = t.contiguous()
+    COPY_STATS["tensors"] += 1
+    COPY_STATS["bytes"] += c.numel() * c.element_size()
+    return c
 
 
 def check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -45,7 +59,7 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
         and all(s % 8 == 0 for s in t.stride()[:-1])
         and t.stride(-1) == 1
     )
-    return t if ok else t.contiguous()
+    return t if ok else _copied(t)
 
 
 def ring_attn_with_lse(
@@ -77,8 +91,8 @@ def ring_attn_with_lse(
     if tq == 0:
         return out, lse
     if k.stride() != v.stride():
-        v = v.contiguous()
-        k = k.contiguous()
+        v = v if v.is_contiguous() else _copied(v)
+        k = k if k.is_contiguous() else _copied(k)
     L = _lib.lib()
     with torch.cuda.device(q.device):
         rc = L.hcp_attn_fwd_lse(
@@ -148,8 +162,8 @@ def ring_attn_merged(
     if tq == 0:
         return output
     if k.stride() != v.stride():
-        v = v.contiguous()
-        k = k.contiguous()
+        v = v if v.is_contiguous() else _copied(v)
+        k = k if k.is_contiguous() else _copied(k)
     L = _lib.lib()
     with torch.cuda.device(q.device):
         rc = L.hcp_attn_fwd_lse_merge(

@@ -54,7 +54,7 @@ import torch
 from . import _lib
 from .kv_cache import reshape_and_cache
 from .merge import merge_attn_states
-from .ring_attn import ring_attn_with_lse
+from .ring_attn import COPY_STATS, ring_attn_with_lse
 from .ring_decode import GrowthBuffer, growth_assignee, local_partial, ring_decode_step
 from .varlen import (
     ENTRY_DTYPE,
@@ -332,6 +332,8 @@ _FAST_IMPLS = ("hip", "triton")
 def reset_impl_stats() -> None:
     for key in IMPL_STATS:
         IMPL_STATS[key] = 0
+    for key in COPY_STATS:
+        COPY_STATS[key] = 0
 
 
 def reset_batch_stats() -> None:

@@ -429,13 +429,27 @@ def choose_split_tokens(seg_lens: list[int], num_kv_heads: int, num_cus: int = 2
     machine), up to ``max_rounds`` once each workgroup would stream more than
     ``round_keys`` keys, so the launch drains evenly while each split stays
     long enough that its fp32 partial is small next to the K/V it summarises.
-    Rounded up to 64 keys.
+    Several rounds: rounded up to 64 keys.  One round: the smallest split
+    whose pieces fill at most one workgroup per CU.
     """
     total = sum(seg_lens) * num_kv_heads
     if total == 0:
         return minimum
     rounds = min(max_rounds, max(1, -(-total // (num_cus * round_keys))))
     s = -(-total // (rounds * num_cus))
+    if rounds == 1:
+        # one round: the smallest split whose pieces (every segment cut into
+        # ceil(len / s) of them) fit the machine, so a single long request
+        # occupies every CU
+        lens = [n for n in seg_lens if n > 0]
+        lo, hi = max(minimum, s), max(max(lens), minimum)
+        while lo < hi:
+            mid = (lo + hi) // 2
+            if sum(-(-n // mid) for n in lens) * num_kv_heads <= num_cus:
+                hi = mid
+            else:
+                lo = mid + 1
+        return min(maximum, lo)
     s = ((s + 63) // 64) * 64
     return max(minimum, min(maximum, s))
 

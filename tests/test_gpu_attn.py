@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from hcp_vllm_plugin_amd import ring_attn_with_lse
+from hcp_vllm_plugin_amd.ring_attn import COPY_STATS
 from oracle import ring_oracle as orc
 from tests._util import LSE_TOL, OUT_TOL, max_err, outlier_k, randn, scale_for
 
@@ -91,8 +92,31 @@ def test_strided_qkv_views(dev):
     t, h, hkv, d = 333, 28, 4, 128
     qkv = randn(gen, (t, h + 2 * hkv, d), torch.bfloat16).to(dev)
     q, k, v = qkv[:, :h], qkv[:, h:h + hkv], qkv[:, h + hkv:]
+    before = dict(COPY_STATS)
     o, lse = ring_attn_with_lse(q, k, v, scale_for(d), 0)
     torch.cuda.synchronize()
+    ro, rl = orc.attn_with_lse(q.float().cpu(), k.float().cpu(), v.float().cpu(), scale_for(d), 0)
+    assert max_err(o, ro) <= OUT_TOL[torch.bfloat16]
+    assert max_err(lse, rl) <= LSE_TOL
+    # these views are loadable in place: no layout copy
+    assert COPY_STATS == before
+
+
+def test_unloadable_layout_is_copied_and_counted(dev):
+    """A head stride that is not a multiple of 8 elements is copied contiguous
+    first (the reference copies every input, ring_backend.py:328); the copy
+    is counted with its bytes, and the result matches the oracle."""
+    gen = torch.Generator().manual_seed(22)
+    t, h, hkv, d = 200, 28, 4, 128
+    qpad = randn(gen, (t, h, d + 4), torch.bfloat16).to(dev)
+    q = qpad[..., :d]  # head stride d + 4: not loadable in place
+    k = randn(gen, (t, hkv, d), torch.bfloat16).to(dev)
+    v = randn(gen, (t, hkv, d), torch.bfloat16).to(dev)
+    before = dict(COPY_STATS)
+    o, lse = ring_attn_with_lse(q, k, v, scale_for(d), 0)
+    torch.cuda.synchronize()
+    assert COPY_STATS["tensors"] == before["tensors"] + 1
+    assert COPY_STATS["bytes"] == before["bytes"] + t * h * d * 2
     ro, rl = orc.attn_with_lse(q.float().cpu(), k.float().cpu(), v.float().cpu(), scale_for(d), 0)
     assert max_err(o, ro) <= OUT_TOL[torch.bfloat16]
     assert max_err(lse, rl) <= LSE_TOL
