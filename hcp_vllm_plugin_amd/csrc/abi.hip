@@ -34,8 +34,8 @@ int check_heads(int32_t h, int32_t hkv, int32_t d, int32_t dtype, const char* wh
   if (h <= 0 || hkv <= 0) return fail(HCP_EINVAL, "%s: num_heads/num_kv_heads must be > 0", who);
   if (h % hkv != 0)
     return fail(HCP_EINVAL, "%s: num_heads (%d) not a multiple of num_kv_heads (%d)", who, h, hkv);
-  if (d < 8 || d > 128 || d % 8)
-    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d not supported (a multiple of 8 up to 128)",
+  if (d < 8 || d > 256 || d % 8)
+    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d not supported (a multiple of 8 up to 256)",
                 who, d);
   if (!dtype16(dtype)) return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
   return HCP_OK;

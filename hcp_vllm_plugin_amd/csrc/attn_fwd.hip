@@ -93,7 +93,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 // rows share the 256-byte bank space, so the row parity takes that role.
 template <int D>
 __device__ __forceinline__ int tile_swz(int row) {
-  if constexpr (D == 128) return 4 * (row & 3) + ((row >> 2) & 3);
+  if constexpr (D >= 128) return 4 * (row & 3) + ((row >> 2) & 3);
   return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
 }
 
@@ -109,7 +109,8 @@ __device__ __forceinline__ i16x4 lds_read_tr(const HCP_LDS(char)* p) {
 
 template <int D, typename T, bool CAUSAL, bool PAGED, bool VARLEN, bool PADDED>
 __global__ __attribute__((amdgpu_flat_work_group_size(kFwdThreads, kFwdThreads),
-                          amdgpu_waves_per_eu(HCP_FWD_WAVES_PER_EU, HCP_FWD_WAVES_PER_EU))) void
+                          amdgpu_waves_per_eu(D == 256 ? 1 : HCP_FWD_WAVES_PER_EU,
+                                              D == 256 ? 1 : HCP_FWD_WAVES_PER_EU))) void
 fa_fwd_kernel(FwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::vec8;
@@ -119,7 +120,10 @@ fa_fwd_kernel(FwdParams p) {
   constexpr int NI = TILEB / (kFwdThreads * 16);  // direct loads per thread per tile
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
-  static_assert(D == 64 || D == 128, "head_dim");
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  // D = 256 runs one wave per SIMD (512 registers): the output accumulator
+  // (128 registers) lives in AGPRs, fed by the PV product directly
+  constexpr bool kAccA = D == 256;
 
   // Two K tiles and two V tiles.  Iteration n reads K(n+1) and V(n) while the
   // loads of K(n+2) and V(n+1) land in the other buffers.
@@ -405,6 +409,16 @@ fa_fwd_kernel(FwdParams p) {
   f32x16 oacc[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) oacc[i] = f32x16{};
+  // AGPR accumulator (D = 256): 24 wait states, ordered against every read
+  // and write of the accumulator (it is an operand), between the products
+  // and other instructions that read or write it
+  auto acc_fence = [&]() __attribute__((always_inline)) {
+    if constexpr (kAccA)
+      asm volatile("s_nop 7\n s_nop 7\n s_nop 7"
+                   : "+a"(oacc[0]), "+a"(oacc[1]), "+a"(oacc[2]), "+a"(oacc[3]),
+                     "+a"(oacc[DBLK > 4 ? 4 : 0]), "+a"(oacc[DBLK > 5 ? 5 : 0]),
+                     "+a"(oacc[DBLK > 6 ? 6 : 0]), "+a"(oacc[DBLK > 7 ? 7 : 0]));
+  };
   f32x16 SA[2], SB[2];  // scores of two tiles (ping-pong), 2 x 32 keys each
   V8 pf[4];             // P^T of the current tile, 16 keys per fragment
 
@@ -473,8 +487,12 @@ fa_fwd_kernel(FwdParams p) {
     const float alpha = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
     l_run *= alpha;
     lr_run *= alpha;
+    // (AGPR accumulator: wait out the last product before the read-back,
+    // and let the write-back land before the next product reads it)
+    acc_fence();
 #pragma unroll
     for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
+    acc_fence();
     m_ref = m_new;
   };
 
@@ -572,9 +590,14 @@ fa_fwd_kernel(FwdParams p) {
         else
           load_one(rs2, i / 2, ldst2);
       }
-      // scores st*EA .. st*EA+EA-1 of the current tile
+      // scores st*EA .. st*EA+EA-1 of the current tile (D = 256: one pair
+      // every second MFMA)
+      if constexpr (EA >= 2) {
 #pragma unroll
-      for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, m_use, ts);
+        for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, m_use, ts);
+      } else if (st & 1) {
+        exp_pair(st >> 1, Sc, m_use, ts);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     // P(n) is complete here: keep its computation in this phase (all its uses
@@ -597,7 +620,10 @@ fa_fwd_kernel(FwdParams p) {
     for (int st = 0; st < NB; ++st) {
       const int t = st / DBLK, db = st % DBLK;
       if (st + HCP_VPF < NB) vf[(st + HCP_VPF) % VR] = vread(st + HCP_VPF);
-      oacc[db] = E::mfma32(as_vec8<V8>(vf[st % VR]), pf[t], oacc[db]);
+      if constexpr (kAccA)
+        E::mfma32_acc(oacc[db], as_vec8<V8>(vf[st % VR]), pf[t]);
+      else
+        oacc[db] = E::mfma32(as_vec8<V8>(vf[st % VR]), pf[t], oacc[db]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -699,6 +725,8 @@ fa_fwd_kernel(FwdParams p) {
   if (n < ntiles) iterate(n, SA, SB, K0, V1, K1, V0);
 
   // ---- epilogue ----
+  // (AGPR accumulator: the last products have landed before it is read)
+  acc_fence();
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float lr_tot = lr_run + __shfl_xor(lr_run, 32);
   // Merge path: this wave's 32 rows of the partial state are fetched whole
@@ -841,6 +869,11 @@ hipError_t launch_fwd(const FwdParams& p, int head_dim, int dtype, bool causal,
   const int64_t grid =
       xcd_grid_size(static_cast<int64_t>(p.num_tiles) * p.group, p.num_kv_heads);
   if (grid <= 0) return hipSuccess;
+  if (head_dim > 128) {  // 136 .. 256: computed in 256 columns, the tail zero
+    return dtype == HCP_DTYPE_BF16
+               ? launch_fwd_d<256, __bf16>(p, grid, causal, paged, varlen, st)
+               : launch_fwd_d<256, _Float16>(p, grid, causal, paged, varlen, st);
+  }
   if (head_dim > 64) {  // 72 .. 128: computed in 128 columns, the tail zero
     return dtype == HCP_DTYPE_BF16
                ? launch_fwd_d<128, __bf16>(p, grid, causal, paged, varlen, st)

@@ -37,6 +37,11 @@ struct Elem<__bf16> {
   static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  // acc += a b with the accumulator kept in AGPRs.  The caller keeps the
+  // wait states around reads and writes of acc by other instructions.
+  static __device__ __forceinline__ void mfma32_acc(f32x16& acc, vec8 a, vec8 b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  }
   static __device__ __forceinline__ uint16_t from_float(float x) {
     __bf16 h = static_cast<__bf16>(x);
     return __builtin_bit_cast(uint16_t, h);
@@ -54,6 +59,9 @@ struct Elem<_Float16> {
   }
   static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ void mfma32_acc(f32x16& acc, vec8 a, vec8 b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
   }
   static __device__ __forceinline__ uint16_t from_float(float x) {
     _Float16 h = static_cast<_Float16>(x);

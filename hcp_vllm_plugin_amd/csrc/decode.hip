@@ -42,9 +42,12 @@ constexpr int kStreamAux = 2;
 
 
 // LDS of the split kernel, shared by its paged and contiguous instantiations.
+// Each wave double-buffers its chunks' K and V rows; D = 256 runs two waves
+// per workgroup so the buffers stay within 128 KB.
 template <int D>
 struct DecShared {
   static constexpr int CHB = kDecChunk * D * 2;  // bytes of a chunk's K (or V) rows
+  static constexpr int W = D == 256 ? 2 : 4;     // waves per workgroup
 };
 
 template <int D, typename T, bool PAGED>
@@ -64,7 +67,8 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
   constexpr int CHB = kDecChunk * ROWB;  // bytes of the K (or V) rows of a chunk
   constexpr int NLD = CHB / 1024;        // LDS-DMA instructions per K (or V) chunk
   constexpr int KPI = 1024 / ROWB;       // key rows per DMA instruction
-  static_assert(D == 64 || D == 128, "head_dim");
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
+  constexpr int W = DecShared<D>::W;  // waves per workgroup
 
   // Wave-private chunk buffers [K rows | V rows] (bufE / bufO: even / odd
   // chunks of the wave, distinct objects so the compiler can tell reads of
@@ -165,18 +169,35 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
           s1 = E::mfma16(as_vec8<V8>(kx), qf[s], s1);
       }
     }
-    // V rows 16(j>>2) + 4g4 + (j&3), d = NU*c16 .. +NU-1
-    u32x4 vc[8];
+    // V rows 16(j>>2) + 4g4 + (j&3), d = NU*c16 .. +NU-1 (NU/2 words)
+    constexpr int VW = NU / 2 < 4 ? 4 : NU / 2;
+    typedef uint32_t vwords __attribute__((ext_vector_type(VW)));
+    vwords vc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int row = 16 * (j >> 2) + 4 * g4 + (j & 3);
       const HCP_LDS_PTR(char) vrow = src + CHB + row * ROWB;
-      if constexpr (NU == 8) {
-        vc[j] = *reinterpret_cast<const HCP_LDS_PTR(u32x4)>(vrow + 16 * (c16 ^ (row % CPR)));
+      if constexpr (NU == 16) {
+        const u32x4 x0 = *reinterpret_cast<const HCP_LDS_PTR(u32x4)>(
+            vrow + 16 * ((2 * c16) ^ (row % CPR)));
+        const u32x4 x1 = *reinterpret_cast<const HCP_LDS_PTR(u32x4)>(
+            vrow + 16 * ((2 * c16 + 1) ^ (row % CPR)));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          vc[j][w] = x0[w];
+          vc[j][4 + w] = x1[w];
+        }
+      } else if constexpr (NU == 8) {
+        const u32x4 x = *reinterpret_cast<const HCP_LDS_PTR(u32x4)>(vrow + 16 * (c16 ^ (row % CPR)));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) vc[j][w] = x[w];
       } else {
         const u32x2 x = *reinterpret_cast<const HCP_LDS_PTR(u32x2)>(
             vrow + 16 * ((c16 >> 1) ^ (row % CPR)) + 8 * (c16 & 1));
-        vc[j] = u32x4{x[0], x[1], 0, 0};
+        vc[j][0] = x[0];
+        vc[j][1] = x[1];
+        vc[j][2] = 0;
+        vc[j][3] = 0;
       }
     }
     if (k0 + kDecChunk > ke) {
@@ -226,7 +247,7 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
     }
   };
 
-  // ---- the wave's chunks wave, wave+4, ...; next chunk's DMA in flight ----
+  // ---- the wave's chunks wave, wave+W, ...; next chunk's DMA in flight ----
   const int64_t nchunks = (ke - kb + kDecChunk - 1) / kDecChunk;
   HCP_LDS_PTR(char) be = (HCP_LDS_PTR(char))(bufE[wave]);
   HCP_LDS_PTR(char) bo = (HCP_LDS_PTR(char))(bufO[wave]);
@@ -315,25 +336,25 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
           }
         }
       };
-      // per step: fetch the ids of chunk ci+8, issue chunk ci+4 (its ids
+      // per step: fetch the ids of chunk ci+2W, issue chunk ci+W (its ids
       // fetched a step ago), wait until only those 3*NLD loads are
       // outstanding -- chunk ci has landed -- and compute it
       auto run_loop = [&](auto buf) __attribute__((always_inline)) {
         fetch_ids(kb + ci * kDecChunk, idA);
-        fetch_ids(next_k0(ci + 4), idB);
+        fetch_ids(next_k0(ci + W), idB);
         issue_p(buf, kb + ci * kDecChunk, idA, be);
         while (true) {
-          fetch_ids(next_k0(ci + 8), idA);
-          issue_p(buf, next_k0(ci + 4), idB, bo);
+          fetch_ids(next_k0(ci + 2 * W), idA);
+          issue_p(buf, next_k0(ci + W), idB, bo);
           wait_vmcnt<3 * NLD>();
           compute(kb + ci * kDecChunk, be);
-          ci += 4;
+          ci += W;
           if (ci >= nchunks) break;
-          fetch_ids(next_k0(ci + 8), idB);
-          issue_p(buf, next_k0(ci + 4), idA, be);
+          fetch_ids(next_k0(ci + 2 * W), idB);
+          issue_p(buf, next_k0(ci + W), idA, be);
           wait_vmcnt<3 * NLD>();
           compute(kb + ci * kDecChunk, bo);
-          ci += 4;
+          ci += W;
           if (ci >= nchunks) break;
         }
       };
@@ -346,20 +367,20 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
   if (!PAGED && ci < nchunks) {
     issue(kb + ci * kDecChunk, be);
     while (true) {
-      issue(next_k0(ci + 4), bo);
+      issue(next_k0(ci + W), bo);
       wait_vmcnt<2 * NLD>();
       compute(kb + ci * kDecChunk, be);
-      ci += 4;
+      ci += W;
       if (ci >= nchunks) break;
-      issue(next_k0(ci + 4), be);
+      issue(next_k0(ci + W), be);
       wait_vmcnt<2 * NLD>();
       compute(kb + ci * kDecChunk, bo);
-      ci += 4;
+      ci += W;
       if (ci >= nchunks) break;
     }
   }
 
-  // ---- combine the 4 waves (the chunk buffers are reused for O) ----
+  // ---- combine the W waves (the chunk buffers are reused for O) ----
   // Each wave's last prefetch (issued unconditionally in the loop) may still
   // be writing bufE/bufO, which sm_o overlays: drain it before the barrier.
   wait_vmcnt<0>();
@@ -377,15 +398,15 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
     for (int r = 0; r < 4; ++r) sm_o[wave][c16][NU * (4 * g4 + r) + u] = oacc[u][r];
   __syncthreads();
 
-  for (int idx = tid; idx < G * D; idx += kDecThreads) {
+  for (int idx = tid; idx < G * D; idx += 64 * W) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][h]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, sm_m[w][h]);
     const float Mu = (M == -INFINITY) ? 0.f : M;
     float L = 0.f, O = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float sc = fast_exp2(sm_m[w][h] - Mu);
       L += sm_l[w][h] * sc;
       O += sm_o[w][h][d] * sc;
@@ -400,14 +421,15 @@ __device__ __forceinline__ void decode_split_body(const DecParams& p, int kvh_in
 // Paged-ness is a property of each entry (a sequence's peer segment is
 // contiguous, its local segment paged), uniform within a workgroup.
 template <int D, typename T>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
+__global__ __attribute__((amdgpu_flat_work_group_size(64 * DecShared<D>::W, 64 * DecShared<D>::W),
                           amdgpu_waves_per_eu(1, 1))) void
 decode_split_kernel(DecParams p) {
   constexpr int CHB = DecShared<D>::CHB;
-  __shared__ __attribute__((aligned(1024))) char bufE[4][2 * CHB];
-  __shared__ __attribute__((aligned(1024))) char bufO[4][2 * CHB];
-  __shared__ float sm_m[4][16];
-  __shared__ float sm_l[4][16];
+  constexpr int W = DecShared<D>::W;
+  __shared__ __attribute__((aligned(1024))) char bufE[W][2 * CHB];
+  __shared__ __attribute__((aligned(1024))) char bufO[W][2 * CHB];
+  __shared__ float sm_m[W][16];
+  __shared__ float sm_l[W][16];
   int kvh;
   int64_t item;
   if (!xcd_remap(blockIdx.x, static_cast<int64_t>(p.num_splits) * p.head_chunks,
@@ -528,7 +550,7 @@ static hipError_t launch_dec_t(const DecParams& dp, const RedParams& rp, hipStre
       xcd_grid_size(static_cast<int64_t>(dp.num_splits) * dp.head_chunks, dp.num_kv_heads);
   if (grid > 0) {
     hipLaunchKernelGGL((decode_split_kernel<D, T>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kDecThreads), 0, st, dp);
+                       dim3(64 * DecShared<D>::W), 0, st, dp);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
@@ -548,6 +570,9 @@ static hipError_t launch_dec_t(const DecParams& dp, const RedParams& rp, hipStre
 
 hipError_t launch_decode(const DecParams& dp, const RedParams& rp, int head_dim,
                          int dtype, hipStream_t st) {
+  if (head_dim > 128)  // 136 .. 256: computed in 256 columns
+    return dtype == HCP_DTYPE_BF16 ? launch_dec_t<256, __bf16>(dp, rp, st)
+                                   : launch_dec_t<256, _Float16>(dp, rp, st);
   if (head_dim > 64)  // 72 .. 128: computed in 128 columns
     return dtype == HCP_DTYPE_BF16 ? launch_dec_t<128, __bf16>(dp, rp, st)
                                    : launch_dec_t<128, _Float16>(dp, rp, st);

@@ -14,9 +14,12 @@ constexpr int kFwdBM = 32 * HCP_FWD_WAVES;  // query rows per prefill workgroup
 constexpr int kFwdBN = 64;                  // keys per prefill tile
 constexpr int kFwdPagedMinBlock = 16;      // paged prefill: rows a wave reads from one block
 
-// Column width the attention kernels compute a head_dim in: 64 or 128 (a
-// smaller head_dim, a multiple of 8, is zero-padded to it inside the kernels).
-__host__ __device__ constexpr int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : 128; }
+// Column width the attention kernels compute a head_dim in: 64, 128 or 256
+// (a smaller head_dim, a multiple of 8, is zero-padded to it inside the
+// kernels).
+__host__ __device__ constexpr int padded_head_dim(int head_dim) {
+  return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
+}
 
 struct FwdParams {
   const void* q;

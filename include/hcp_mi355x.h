@@ -41,7 +41,7 @@ extern "C" {
 typedef enum hcp_status {
   HCP_OK = 0,
   HCP_EINVAL = -1,       /* bad argument: null pointer, negative size, H % Hkv != 0, ... */
-  HCP_EUNSUPPORTED = -2, /* valid but not built: head_dim not a multiple of 8 up to 128, dtype, ... */
+  HCP_EUNSUPPORTED = -2, /* valid but not built: head_dim not a multiple of 8 up to 256, dtype, ... */
   HCP_ELAUNCH = -3,      /* the HIP runtime rejected a launch */
   HCP_EWORKSPACE = -4    /* caller workspace smaller than required */
 } hcp_status;
@@ -126,9 +126,9 @@ const char* hcp_last_error(void);
  * reference's Triton path has no window and falls back to torch for it
  * (:315-323).  window = 0: none.
  * dtype: HCP_DTYPE_F16 or HCP_DTYPE_BF16 for q/k/v/out.  head_dim: any
- * multiple of 8 up to 128 (the reference takes any head_dim, padding it to a
+ * multiple of 8 up to 256 (the reference takes any head_dim, padding it to a
  * power of two with masked columns, ring_triton_attn.py:69-78,201; here the
- * kernels compute in 64 or 128 columns whose tail they load as zeros and
+ * kernels compute in 64, 128 or 256 columns whose tail they load as zeros and
  * never store).  The same holds for every attention entry point below.
  */
 int hcp_attn_fwd_lse(const void* q, const void* k, const void* v, void* out,
@@ -254,7 +254,7 @@ int hcp_plan_decode_splits(const hcp_varlen_entry* entries,
                            int32_t cap, int32_t* seq_partial_start);
 
 /* Bytes of workspace hcp_decode_splitkv needs for `num_splits` partials
- * (kept at the kernel's 64- or 128-column width). */
+ * (kept at the kernel's 64-, 128- or 256-column width). */
 size_t hcp_decode_workspace_bytes(int32_t num_splits, int32_t num_heads,
                                   int32_t head_dim);
 

@@ -209,7 +209,7 @@ def _fwd(L, **kw):
 def test_argument_validation_status_codes(L):
     assert _fwd(L, h=6, hkv=4) == _lib.HCP_EINVAL
     assert b"multiple" in L.hcp_last_error()
-    assert _fwd(L, d=136) == _lib.HCP_EUNSUPPORTED
+    assert _fwd(L, d=264) == _lib.HCP_EUNSUPPORTED
     assert _fwd(L, dtype=_lib.DTYPE_F32) == _lib.HCP_EUNSUPPORTED
     assert _fwd(L, tq=-1) == _lib.HCP_EINVAL
     assert _fwd(L, scale=float("nan")) == _lib.HCP_EINVAL
@@ -259,7 +259,7 @@ def test_attn_merge_status_codes(L):
     assert _fwd_merge(L, acc=24) == _lib.HCP_EINVAL        # not 16-byte aligned
     assert b"aligned" in L.hcp_last_error()
     assert _fwd_merge(L, acc_st=12) == _lib.HCP_EINVAL     # stride not a multiple of 8
-    assert _fwd_merge(L, d=136) == _lib.HCP_EUNSUPPORTED
+    assert _fwd_merge(L, d=264) == _lib.HCP_EUNSUPPORTED
     assert _fwd_merge(L, window=-1) == _lib.HCP_EINVAL
     assert _fwd_merge(L, tq=0) == _lib.HCP_OK               # nothing to do, nothing launched
     assert _fwd(L, lse=None) == _lib.HCP_EINVAL
@@ -287,7 +287,7 @@ def test_decode_splitkv_acc_status_codes(L):
     assert b"null accumulator" in L.hcp_last_error()
     assert _dec_acc(L, acc_lse=None) == _lib.HCP_EINVAL
     assert _dec_acc(L, acc_o=17) == _lib.HCP_EINVAL       # odd address
-    assert _dec_acc(L, d=136) == _lib.HCP_EUNSUPPORTED
+    assert _dec_acc(L, d=264) == _lib.HCP_EUNSUPPORTED
     assert _dec_acc(L, h=30) == _lib.HCP_EINVAL           # not a multiple of hkv
     assert _dec_acc(L, scale=0.0) == _lib.HCP_EINVAL
     assert _dec_acc(L, seqs=0) == _lib.HCP_OK              # nothing to do, nothing launched
@@ -311,7 +311,7 @@ def test_decode_noalloc_limit_and_status_codes(L):
     assert fit == 1161
     assert call(splits=fit + 1) == _lib.HCP_EWORKSPACE
     assert b"fixed scratch" in L.hcp_last_error()
-    assert call(d=136) == _lib.HCP_EUNSUPPORTED
+    assert call(d=264) == _lib.HCP_EUNSUPPORTED
     assert call(h=30) == _lib.HCP_EINVAL
     assert call(dtype=_lib.DTYPE_F32) == _lib.HCP_EUNSUPPORTED
     assert call(splits=-1) == _lib.HCP_EINVAL
@@ -355,6 +355,6 @@ def test_reshape_and_cache_status_codes(L):
 
 
 def test_check_raises_runtime_error_with_library_text(L):
-    rc = _fwd(L, d=136)
-    with pytest.raises(RuntimeError, match="EUNSUPPORTED.*head_dim 136"):
+    rc = _fwd(L, d=264)
+    with pytest.raises(RuntimeError, match="EUNSUPPORTED.*head_dim 264"):
         _lib.check(rc, "hcp_attn_fwd_lse")

@@ -127,10 +127,10 @@ def test_invalid_arguments_raise(dev):
     k = torch.randn(8, 4, 128, device=dev).to(torch.bfloat16)
     with pytest.raises(ValueError):
         ring_attn_with_lse(q, k, k, 0.1, 0)  # 6 % 4 != 0
-    q = torch.randn(8, 4, 136, device=dev).to(torch.bfloat16)
-    k = torch.randn(8, 4, 136, device=dev).to(torch.bfloat16)
+    q = torch.randn(8, 4, 264, device=dev).to(torch.bfloat16)
+    k = torch.randn(8, 4, 264, device=dev).to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="EUNSUPPORTED"):
-        ring_attn_with_lse(q, k, k, 0.1, 0)  # head_dim above 128 not built
+        ring_attn_with_lse(q, k, k, 0.1, 0)  # head_dim above 256 not built
 
 
 def test_deterministic_repeat(dev):

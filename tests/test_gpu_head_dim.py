@@ -2,10 +2,12 @@
 
 The reference kernel takes any head_dim (BLOCK_D = next power of two with the
 columns past head_dim masked, ring_triton_attn.py:69-78,201).  The HIP
-kernels compute in 64 or 128 columns and treat the tail as zeros: every entry
-point is checked here against the oracle at head_dims that are multiples of 8
-below 128 -- the plain and merging forward passes, the paged varlen pass, the
-split-KV decode, the paged KV write and the backend's forward.  Rows are
+kernels compute in 64, 128 or 256 columns and treat the tail as zeros: every
+entry point is checked here against the oracle at head_dims that are
+multiples of 8 up to 256 other than 64 and 128 (256 itself runs the
+one-wave-per-SIMD prefill and two-wave decode instantiations) -- the plain and
+merging forward passes, the paged varlen pass, the split-KV decode, the paged
+KV write and the backend's forward.  Rows are
 packed at their true width ([T, H, head_dim], stride head_dim), so a load
 past a row's end would read the neighbouring head or token and show.
 """
@@ -28,7 +30,7 @@ from tests.test_gpu_varlen import _build as varlen_build
 
 pytestmark = pytest.mark.gpu
 
-DIMS = [8, 40, 72, 80, 96, 112]
+DIMS = [8, 40, 72, 80, 96, 112, 136, 200, 256]
 
 
 @pytest.mark.parametrize("d", DIMS)
@@ -49,7 +51,7 @@ def test_forward_head_dims(dev, d, dtype, off):
     assert max_err(lse, rl) <= LSE_TOL
 
 
-@pytest.mark.parametrize("d", [40, 96])
+@pytest.mark.parametrize("d", [40, 96, 256])
 def test_merged_pass_head_dims(dev, d):
     """Local pass merging a peer partial (the acc epilogue) equals pass +
     merge_attn_states bit for bit, and the oracle's merge within tolerance."""
@@ -73,7 +75,7 @@ def test_merged_pass_head_dims(dev, d):
 
 
 @pytest.mark.parametrize("layout", ["v031", "v023"])
-@pytest.mark.parametrize("d", [80, 40])
+@pytest.mark.parametrize("d", [80, 40, 192, 256])
 def test_varlen_paged_head_dims(dev, layout, d):
     h, hkv, bs, dtype = 28, 4, 16, torch.bfloat16
     lens, peers = [300, 1, 129, 64], [512, 48, 0, 32]
@@ -110,7 +112,10 @@ def test_varlen_paged_head_dims(dev, layout, d):
 
 @pytest.mark.parametrize("h,hkv,d,dtype", [(28, 4, 96, torch.bfloat16),
                                           (14, 2, 80, torch.float16),
-                                          (32, 1, 40, torch.bfloat16)])
+                                          (32, 1, 40, torch.bfloat16),
+                                          (16, 8, 256, torch.bfloat16),
+                                          (24, 2, 256, torch.float16),
+                                          (8, 1, 184, torch.bfloat16)])
 @pytest.mark.parametrize("split", [None, 64])
 def test_decode_head_dims(dev, h, hkv, d, dtype, split):
     decode_case(dev, h, hkv, d, dtype, peer_lens=[1500, 0, 64], loc_lens=[300, 800, 1],
@@ -118,7 +123,7 @@ def test_decode_head_dims(dev, h, hkv, d, dtype, split):
 
 
 @pytest.mark.parametrize("layout", ["v031", "v023"])
-@pytest.mark.parametrize("d", [96, 40, 200])
+@pytest.mark.parametrize("d", [96, 40, 200, 256])
 def test_cache_write_head_dims(dev, layout, d):
     cache, key, value, slots = cache_case(layout, torch.bfloat16, torch.int64, 333, 41, 16, 4,
                                           d, 90 + d)
@@ -130,7 +135,7 @@ def test_cache_write_head_dims(dev, layout, d):
     assert torch.equal(dcache.cpu(), ref)
 
 
-@pytest.mark.parametrize("d", [96, 80])
+@pytest.mark.parametrize("d", [96, 80, 256])
 def test_backend_forward_head_dims(dev, d):
     """HcpRingAttentionImpl.forward at head_size d: prefill rows (with a
     staged peer chunk) and a decode row, paged cache [nb, Hkv, 16, 2d]."""
