@@ -607,6 +607,51 @@ def bench_ring_decode_hop(dev, steps, warmup, seed=6, chunk=32768, growth=512):
     }
 
 
+def bench_head_dim_256(dev, steps, warmup, seed=7, n=8192, seqs=32, keys=32768):
+    """head_dim 256 (a Gemma-2-9B-like attention shape: 16 query heads, 8 KV
+    heads, bf16): the ring prefill step (8192 peer keys non-causal, then 8192
+    local causal keys merging the peer result) and a split-KV decode of 32
+    sequences x 32768 staged keys.  Runs the one-wave-per-SIMD prefill and the
+    two-wave decode instantiations; a widening line, not a headline."""
+    from hcp_vllm_plugin_amd import ring_attn_merged, ring_attn_with_lse
+    from hcp_vllm_plugin_amd.varlen import DecodeBatch, head_major, segment_contiguous
+
+    h, hkv, d = 16, 8, 256
+    sc = 1.0 / math.sqrt(d)
+    dgen = torch.Generator(device=dev).manual_seed(seed)
+
+    def rn(*shape):
+        return torch.randn(*shape, generator=dgen, device=dev).to(torch.bfloat16)
+
+    q, kl, vl, kp, vp = rn(n, h, d), rn(n, hkv, d), rn(n, hkv, d), rn(n, hkv, d), rn(n, hkv, d)
+    out = torch.empty_like(q)
+
+    def step():
+        o_p, l_p = ring_attn_with_lse(q, kp, vp, sc, None)
+        ring_attn_merged(q, kl, vl, sc, 0, o_p, l_p, output=out)
+
+    ms = timed(step, steps, warmup)
+    flops = 4 * d * h * (n * n + causal_pairs(n, n, 0))
+    del q, kl, vl, kp, vp, out
+    kd, vd = head_major(rn(seqs * keys, hkv, d)), head_major(rn(seqs * keys, hkv, d))
+    qd = rn(seqs, h, d)
+    batch = DecodeBatch([[segment_contiguous(kd, vd, s * keys, keys)] for s in range(seqs)],
+                        h, hkv, d, dev)
+    od = torch.empty_like(qd)
+    dms = timed(lambda: batch.run(qd, od, None, sc), steps, warmup)
+    dbytes = seqs * keys * hkv * d * 2 * 2 + seqs * h * d * 2 * 2
+    return {
+        "workload": (f"head_dim 256 (16 / 8 heads, bf16): ring prefill step {n} peer + {n} "
+                     f"local causal keys merged; decode {seqs} x {keys} staged keys"),
+        "prefill_ms": round(ms, 4),
+        "prefill_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "prefill_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "decode_ms": round(dms, 4),
+        "decode_gbs": round(dbytes / (dms * 1e-3) / 1e9, 1),
+        "decode_frac_hbm": round(dbytes / (dms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+    }
+
+
 def bench_llama70b(dev, steps, warmup, seed=4, n=65536, chunk=8192):
     """Long-context layer at the Llama-3-70B attention shape (64 / 8 heads,
     head_dim 128), bf16: 65536 local query tokens causal over local keys
@@ -802,7 +847,7 @@ def main():
                     help="skip the varlen and 70B long-context measurements")
     ap.add_argument("--part", choices=("all", "prefill", "decode", "varlen", "llama70b",
                                        "kvwrite", "ingest", "ringdec", "window", "pdecode",
-                                       "fdecode", "copy"),
+                                       "fdecode", "d256", "copy"),
                     default="all",
                     help="run one part only (profiler passes); the JSON line needs 'all'")
     args = ap.parse_args()
@@ -841,6 +886,9 @@ def main():
     if args.part == "ringdec":
         print(json.dumps(bench_ring_decode_hop(dev, args.steps, args.warmup)), flush=True)
         return
+    if args.part == "d256":
+        print(json.dumps(bench_head_dim_256(dev, args.steps, args.warmup)), flush=True)
+        return
     if args.part == "kvwrite":
         print(json.dumps(bench_kv_cache_write(dev, args.steps, args.warmup)), flush=True)
         return
@@ -862,6 +910,7 @@ def main():
         extra["sliding_window"] = bench_sliding_window(dev, args.steps, args.warmup)
         extra["decode_paged"] = bench_decode_paged(dev, args.steps, args.warmup)
         extra["decode_forward_staged"] = bench_decode_forward(dev, args.steps, args.warmup)
+        extra["head_dim_256"] = bench_head_dim_256(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = load_traffic()
 
