@@ -177,3 +177,57 @@ def test_backend_forward_head_dims(dev, d):
                            peers=[(kp.float(), vp.float()), None, None],
                            out_dtype=torch.float32)
     assert max_err(out, ref) <= OUT_TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("off", [None, 1500])
+@pytest.mark.parametrize("slope,spike", [(2.0, None), (0.0, 1500)])
+def test_rescale_path_d256(dev, dtype, off, slope, spike):
+    """Scores rising far above every row's first tile at head_dim 256: the
+    rescale of the output accumulator, which at this width lives in AGPRs,
+    runs on most rows (inputs as in test_gpu_attn's drift cases)."""
+    from tests.test_gpu_attn import _drift_inputs
+
+    tq, tk, h, hkv, d = 300, 2048, 8, 2, 256
+    gen = torch.Generator().manual_seed(int(slope * 10) + 7 * (off or 0) + 256)
+    q, k, v = _drift_inputs(gen, tq, tk, h, hkv, d, dtype, slope, spike)
+    scale = scale_for(d)
+    o, lse = ring_attn_with_lse(q.to(dev), k.to(dev), v.to(dev), scale, off)
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_with_lse(q.float(), k.float(), v.float(), scale, off)
+    assert max_err(o, ro) <= OUT_TOL[dtype]
+    assert max_err(lse, rl) <= LSE_TOL
+
+
+def test_ring_step_d256_full_size(dev):
+    """The head_dim 256 bench shape (16 / 8 heads, bf16): the 8192-key peer
+    pass, then the 8192-key local causal pass merging it; sampled rows against
+    the oracle, and the whole output against one causal pass over [peer; local]
+    (the ring step's identity)."""
+    h, hkv, d, n = 16, 8, 256, 8192
+    g = torch.Generator(device=dev).manual_seed(256)
+    ch = torch.randperm(d, generator=torch.Generator().manual_seed(3))[:4]
+
+    def draw(shape, outlier=False):
+        x = torch.randn(*shape, generator=g, device=dev)
+        if outlier:
+            x[..., ch] *= 8.0
+        return x.to(torch.bfloat16)
+
+    q = draw((n, h, d))
+    kl, vl, kp, vp = draw((n, hkv, d), True), draw((n, hkv, d)), draw((n, hkv, d), True), draw((n, hkv, d))
+    scale = scale_for(d)
+    o_p, l_p = ring_attn_with_lse(q, kp, vp, scale, None)
+    lse = torch.empty(h, n, dtype=torch.float32, device=dev)
+    out = ring_attn_merged(q, kl, vl, scale, 0, o_p, l_p, output_lse=lse)
+    kk, vv = torch.cat([kp, kl]), torch.cat([vp, vl])
+    o1, l1 = ring_attn_with_lse(q, kk, vv, scale, n)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    assert max_err(out, o1) <= 2 * OUT_TOL[torch.bfloat16]
+    assert max_err(lse, l1) <= 2 * LSE_TOL
+    kc, vc = kk.float().cpu(), vv.float().cpu()
+    for r0 in (0, 3000, 8176):
+        ro, rl = orc.attn_with_lse(q[r0:r0 + 16].float().cpu(), kc, vc, scale, n + r0)
+        assert max_err(out[r0:r0 + 16], ro) <= OUT_TOL[torch.bfloat16], r0
+        assert max_err(lse[:, r0:r0 + 16], rl) <= LSE_TOL, r0
