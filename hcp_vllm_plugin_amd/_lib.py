@@ -60,9 +60,10 @@ EXPORTED_SYMBOLS = (
     "hcp_decode_splitkv_noalloc",
     "hcp_merge_attn_states",
     "hcp_reshape_and_cache",
+    "hcp_gather_paged_kv",
 )
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class KvSegment(ctypes.Structure):
@@ -184,6 +185,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.hcp_reshape_and_cache.argtypes = [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I32, _I64, _I32, _I32, _P, _I32, _P,
     ]
+    lib.hcp_gather_paged_kv.restype = ctypes.c_int
+    lib.hcp_gather_paged_kv.argtypes = [_P, _I32, _P, _I64, _I32, _I32, _I32, _P, _P, _P]
     lib.hcp_merge_attn_states.restype = ctypes.c_int
     lib.hcp_merge_attn_states.argtypes = [
         _P, _I64, _I64, _I32, _P, _I64,

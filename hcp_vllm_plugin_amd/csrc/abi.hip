@@ -643,4 +643,37 @@ int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok, int64_t k_strid
                        who);
 }
 
+int hcp_gather_paged_kv(const hcp_varlen_entry* entries, int32_t num_entries,
+                        const int64_t* out_start, int64_t max_len, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t dtype, void* k_out, void* v_out,
+                        void* stream) {
+  const char* who = "hcp_gather_paged_kv";
+  if (num_entries < 0 || max_len < 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return fail(HCP_EINVAL, "%s: bad sizes", who);
+  if (head_dim % 8 || head_dim > 256)
+    return fail(HCP_EUNSUPPORTED, "%s: head_dim %d not supported (a multiple of 8 up to 256)",
+                who, head_dim);
+  if (!dtype16(dtype)) return fail(HCP_EUNSUPPORTED, "%s: dtype %d not supported", who, dtype);
+  if (num_entries > 65535) return fail(HCP_EINVAL, "%s: more than 65535 entries", who);
+  if (num_entries == 0 || max_len == 0) return HCP_OK;
+  if (!entries || !out_start || !k_out || !v_out) return fail(HCP_EINVAL, "%s: null pointer", who);
+  if (!aligned8(entries) || !aligned8(out_start) || !aligned16(k_out) || !aligned16(v_out))
+    return fail(HCP_EINVAL, "%s: misaligned pointer", who);
+  if (max_len * num_kv_heads > (int64_t)INT32_MAX * 16)
+    return fail(HCP_EINVAL, "%s: too many rows", who);
+  hcp::GatherParams p{};
+  p.entries = entries;
+  p.out_start = out_start;
+  p.max_len = max_len;
+  p.num_entries = num_entries;
+  p.num_kv_heads = num_kv_heads;
+  p.cpr = head_dim / 8;
+  p.cpr_shift = (p.cpr & (p.cpr - 1)) ? -1 : 31 - __builtin_clz(static_cast<unsigned>(p.cpr));
+  p.head_dim = head_dim;
+  p.k_out = k_out;
+  p.v_out = v_out;
+  (void)dtype;  // a 16-bit copy: the bytes are moved as they are
+  return launch_status(hcp::launch_gather(p, static_cast<hipStream_t>(stream)), who);
+}
+
 }  // extern "C"

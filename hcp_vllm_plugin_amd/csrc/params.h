@@ -114,11 +114,27 @@ struct CacheParams {
   int32_t bs_shift, bs_mask;
 };
 
+// Gather of paged KV segments into one contiguous [total, Hkv, D] K and V
+// (prefill over caches with blocks shorter than a wave's 16 rows).
+struct GatherParams {
+  const hcp_varlen_entry* entries;  // device: paged segments
+  const int64_t* out_start;         // device: first output token of each entry
+  int64_t max_len;                  // longest segment
+  int32_t num_entries;
+  int32_t num_kv_heads;
+  int32_t cpr;        // head_dim / 8: 16-byte chunks per row
+  int32_t cpr_shift;  // log2(cpr) when cpr is a power of two, else -1
+  int32_t head_dim;
+  void* k_out;
+  void* v_out;
+};
+
 hipError_t launch_fwd(const FwdParams& p, int head_dim, int dtype, bool causal,
                       bool paged, bool varlen, hipStream_t st);
 hipError_t launch_decode(const DecParams& dp, const RedParams& rp, int head_dim,
                          int dtype, hipStream_t st);
 hipError_t launch_merge(const MergeParams& p, hipStream_t st);
 hipError_t launch_cache_write(const CacheParams& p, bool slots_i64, hipStream_t st);
+hipError_t launch_gather(const GatherParams& p, hipStream_t st);
 
 }  // namespace hcp

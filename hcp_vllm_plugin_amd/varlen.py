@@ -285,6 +285,11 @@ def plan_varlen_tiles(entries: list[VarlenEntry], causal: bool) -> list[tuple[in
     return [(tiles[2 * i], tiles[2 * i + 1]) for i in range(rc)]
 
 
+# smallest block_size the paged prefill kernel reads in place (a wave's 16
+# rows of a tile must lie in one block); smaller ones are gathered first
+_MIN_PAGED_BLOCK = 16
+
+
 class VarlenLaunch:
     """A planned varlen launch: entries and tile list uploaded to the device.
 
@@ -319,13 +324,65 @@ class VarlenLaunch:
             # the entries point at K/V / cache / block-table storage by
             # address: hold those tensors for as long as this launch can run
             self._keep = [getattr(e, "_keep", None) for e in entries]
+        # Paged prefill reads a wave's 16 rows of a tile from one block: over a
+        # cache with shorter blocks the segments are gathered into one
+        # contiguous K/V buffer on the device first (hcp_gather_paged_kv, one
+        # launch per run), and the attention runs over that copy.
+        self._gather = None
+        if self.paged and self.num_entries:
+            host = np.frombuffer(arr, dtype=ENTRY_DTYPE, count=self.num_entries).copy()
+            if int(host["block_size"].min()) < _MIN_PAGED_BLOCK:
+                lens = host["len"].astype(np.int64)
+                out_start = np.zeros(self.num_entries, dtype=np.int64)
+                out_start[1:] = np.cumsum(lens)[:-1]
+                cont = host.copy()
+                for f in ("block_table", "stride_block", "block_size", "num_blocks",
+                          "k_addr", "v_addr"):
+                    cont[f] = 0
+                cont["start"] = out_start
+                self._gather = {"paged": host, "out_start": out_start, "cont": cont,
+                                "total": int(lens.sum()), "max_len": int(lens.max()),
+                                "shape": None}
+                arr = cont
+                self.paged = False
         tiles = (ctypes.c_int32 * max(2 * cap, 2))()
         rc = L.hcp_plan_varlen_tiles(_nbytes_addr(arr)[1], self.num_entries,
                                      int(self.causal), bm, ctypes.addressof(tiles), cap)
         _lib.check(rc, "hcp_plan_varlen_tiles")
         self.num_tiles = rc
-        self._plan_dev, (self.entries_ptr, self.tiles_ptr) = _upload([arr, tiles], device)
+        if self._gather is None:
+            self._plan_dev, (self.entries_ptr, self.tiles_ptr) = _upload([arr, tiles], device)
+        else:
+            g = self._gather
+            self._plan_dev, (g["paged_ptr"], g["start_ptr"], self.tiles_ptr) = _upload(
+                [g["paged"], g["out_start"], tiles], device)
+            self.entries_ptr = None
         self.device = device
+
+    def _gathered(self, q: torch.Tensor, num_kv_heads: int) -> None:
+        """Gather mode: copy every entry's paged keys into the contiguous
+        buffer (allocated, and the contiguous entries uploaded, on the first
+        run of a shape), on the current stream."""
+        g = self._gather
+        head_dim = q.shape[2]
+        shape = (num_kv_heads, head_dim, q.dtype)
+        if g["shape"] != shape:
+            k = torch.empty(max(g["total"], 1), num_kv_heads, head_dim, dtype=q.dtype,
+                            device=q.device)
+            v = torch.empty_like(k)
+            cont = g["cont"].copy()
+            cont["k_addr"] = k.data_ptr()
+            cont["v_addr"] = v.data_ptr()
+            cont["stride_tok"] = num_kv_heads * head_dim
+            cont["stride_head"] = head_dim
+            g["k"], g["v"], g["shape"] = k, v, shape
+            g["cont_dev"], (self.entries_ptr,) = _upload([cont], q.device)
+        L = _lib.lib()
+        rc = L.hcp_gather_paged_kv(g["paged_ptr"], self.num_entries, g["start_ptr"],
+                                   g["max_len"], num_kv_heads, head_dim,
+                                   _lib.dtype_code(q.dtype), g["k"].data_ptr(),
+                                   g["v"].data_ptr(), _lib.stream_ptr(q.device))
+        _lib.check(rc, "hcp_gather_paged_kv")
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
             num_kv_heads: int, scale: float, window: int | None = None,
@@ -346,6 +403,8 @@ class VarlenLaunch:
         L = _lib.lib()
         win = int(window or 0) if self.causal else 0
         with torch.cuda.device(q.device):
+            if self._gather is not None:
+                self._gathered(q, num_kv_heads)
             if acc is None:
                 rc = L.hcp_attn_fwd_varlen(
                     q.data_ptr(), q.stride(0), q.stride(1),

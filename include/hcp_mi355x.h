@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define HCP_ABI_VERSION 8
+#define HCP_ABI_VERSION 9
 
 typedef enum hcp_status {
   HCP_OK = 0,
@@ -67,8 +67,9 @@ typedef enum hcp_dtype {
  * stride_block = 2*bs*Hkv*D, stride_head = D, stride_tok = Hkv*D;
  * ring_backend.py:601,617-624).  num_blocks (0: unknown) bounds the block ids
  * the kernels read: a larger id reads the cache's last block (or, for decode
- * over a cache under 4 GiB, zeros) instead of memory outside it.  Paged prefill needs
- * block_size >= 16 (hcp_plan_varlen_tiles checks it).
+ * over a cache under 4 GiB, zeros) instead of memory outside it.  Paged prefill
+ * reads block_size >= 16 in place (hcp_plan_varlen_tiles checks it); smaller
+ * blocks are first gathered contiguous with hcp_gather_paged_kv.
  */
 typedef struct hcp_kv_segment {
   uint64_t k_addr;
@@ -415,6 +416,26 @@ int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok,
                           int64_t num_tokens, int32_t num_kv_heads,
                           int32_t head_dim, const hcp_paged_cache* cache,
                           int32_t dtype, void* stream);
+
+/*
+ * Gather of paged KV segments into contiguous K and V: entry e's keys
+ * [kv.start, kv.start + kv.len) of its block frame become rows
+ * out_start[e] .. out_start[e] + kv.len - 1 of k_out / v_out, each
+ * [total, Hkv, head_dim] contiguous (token stride Hkv * head_dim).  The
+ * reference gathers every request's local KV this way before attention
+ * (ring_backend.py:617-624); here it serves only paged prefill over caches
+ * with block_size < 16, whose blocks are shorter than the rows the prefill
+ * kernel reads from one block (hcp_plan_varlen_tiles refuses those), and runs
+ * the whole batch in one launch.  `entries` (paged: block_table != 0) and
+ * `out_start` (int64) are DEVICE arrays; at most 65535 entries, none longer
+ * than max_len.  Block ids at or past kv.num_blocks (when given) are clamped
+ * to the last block.  head_dim a multiple of 8 up to 256; k_out / v_out
+ * 16-byte aligned.
+ */
+int hcp_gather_paged_kv(const hcp_varlen_entry* entries, int32_t num_entries,
+                        const int64_t* out_start, int64_t max_len,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                        void* k_out, void* v_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -358,3 +358,20 @@ def test_check_raises_runtime_error_with_library_text(L):
     rc = _fwd(L, d=264)
     with pytest.raises(RuntimeError, match="EUNSUPPORTED.*head_dim 264"):
         _lib.check(rc, "hcp_attn_fwd_lse")
+
+
+def test_gather_paged_kv_status_codes(L):
+    """Argument checks of hcp_gather_paged_kv, all before any device work."""
+    g = L.hcp_gather_paged_kv
+    # nothing to do: no entries, or no keys
+    assert g(0, 0, 0, 0, 4, 128, _lib.DTYPE_BF16, 0, 0, 0) == 0
+    assert g(16, 3, 16, 0, 4, 128, _lib.DTYPE_BF16, 16, 16, 0) == 0
+    assert g(16, 3, 16, 10, 0, 128, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EINVAL
+    assert g(16, -1, 16, 10, 4, 128, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EINVAL
+    assert g(16, 3, 16, 10, 4, 132, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EUNSUPPORTED
+    assert g(16, 3, 16, 10, 4, 264, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EUNSUPPORTED
+    assert g(16, 3, 16, 10, 4, 128, _lib.DTYPE_F32, 16, 16, 0) == _lib.HCP_EUNSUPPORTED
+    assert g(0, 3, 16, 10, 4, 128, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EINVAL  # null
+    assert g(16, 3, 16, 10, 4, 128, _lib.DTYPE_BF16, 8, 16, 0) == _lib.HCP_EINVAL  # align
+    assert g(16, 70000, 16, 10, 4, 128, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EINVAL
+    assert "hcp_gather_paged_kv" in L.hcp_last_error().decode()

@@ -33,14 +33,14 @@ def _meta(dev, qsl, seq_lens, bt):
     )
 
 
-def _cache(gen, layout, nb, dtype):
+def _cache(gen, layout, nb, dtype, bs=BS):
     if layout == "v031":
-        return randn(gen, (nb, HKV, BS, 2 * D), dtype)
-    return randn(gen, (nb, 2, BS, HKV, D), dtype)
+        return randn(gen, (nb, HKV, bs, 2 * D), dtype)
+    return randn(gen, (nb, 2, bs, HKV, D), dtype)
 
 
-def _block_table(gen, seq_lens, nb):
-    blocks = [-(-tk // BS) for tk in seq_lens]
+def _block_table(gen, seq_lens, nb, bs=BS):
+    blocks = [-(-tk // bs) for tk in seq_lens]
     perm = torch.randperm(nb, generator=gen).to(torch.int32)
     bt = torch.zeros(len(seq_lens), max(blocks) + 1, dtype=torch.int32)
     o = 0
@@ -61,7 +61,7 @@ def _clean(monkeypatch):
 
 
 def _run(dev, layout, reqs, dtype=torch.bfloat16, seed=61, split=0, staged_chunks=None,
-         monkeypatch=None, window=None):
+         monkeypatch=None, window=None, bs=BS):
     """reqs: list of (tq, tk).  staged_chunks: per request list of chunk lengths
     (peer prefix = their concatenation) or None."""
     gen = torch.Generator().manual_seed(seed)
@@ -69,9 +69,9 @@ def _run(dev, layout, reqs, dtype=torch.bfloat16, seed=61, split=0, staged_chunk
     qsl = [0]
     for tq, _ in reqs:
         qsl.append(qsl[-1] + tq)
-    nb = sum(-(-tk // BS) for tk in seq_lens) + 4
-    cache = _cache(gen, layout, nb, dtype)
-    bt = _block_table(gen, seq_lens, nb)
+    nb = sum(-(-tk // bs) for tk in seq_lens) + 4
+    cache = _cache(gen, layout, nb, dtype, bs)
+    bt = _block_table(gen, seq_lens, nb, bs)
     query = randn(gen, (qsl[-1] + 5, H, D), dtype)  # 5 padding rows past num_actual
     peers = None
     impl = rb.HcpRingAttentionImpl(H, D, scale_for(D), HKV, sliding_window=window)
@@ -113,6 +113,22 @@ def _run(dev, layout, reqs, dtype=torch.bfloat16, seed=61, split=0, staged_chunk
 def test_forward_no_peer_is_causal_over_paged_cache(dev, layout):
     _run(dev, layout, [(300, 300), (17, 517), (1, 40), (0, 64), (129, 1000)])
     assert rb.IMPL_STATS["attn_hip"] == 1 and rb.IMPL_STATS["merge_hip"] == 0
+    assert rb.IMPL_STATS["attn_torch"] == 0
+
+
+@pytest.mark.parametrize("bs", [1, 8])
+@pytest.mark.parametrize("layout", ["v031", "v023"])
+def test_forward_small_blocks(dev, layout, bs, monkeypatch):
+    """Caches with blocks under 16 tokens: prefill gathers the local segments
+    on the device first (the reference gathers for every block size,
+    ring_backend.py:617-624), decode reads them in place; staged peers and a
+    split of the local cache both run."""
+    reqs = [(300, 300 + 64), (17, 517), (1, 40), (129, 1000)]
+    _run(dev, layout, reqs, staged_chunks=[[64], None, None, None], bs=bs)
+    rb.clear_peer_kv()
+    _run(dev, layout, [(200, 700), (1, 333), (64, 900)], split=100, monkeypatch=monkeypatch,
+         bs=bs)
+    _run(dev, layout, [(1, 700), (1, 33), (1, 1500)], bs=bs)  # a decode batch
     assert rb.IMPL_STATS["attn_torch"] == 0
 
 

@@ -163,3 +163,82 @@ def test_varlen_paged_cache_past_4gib_nan_outside_segments(dev, causal):
         assert max_err(lse[:, sl], rl) <= LSE_TOL, r
         qs += ln
     del cache
+
+
+@pytest.mark.parametrize("bs", [1, 4, 8])
+@pytest.mark.parametrize("layout", ["v031", "v023"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_paged_small_blocks(dev, bs, layout, causal):
+    """Caches with blocks shorter than 16 tokens (the reference's gather takes
+    any block size, ring_backend.py:617-624): the launch gathers the paged
+    segments into one contiguous buffer on the device and attends over it.
+    Segments start mid-block; one entry is empty; the run is repeated after
+    the cache changes, so the gather reads the cache at run time."""
+    from hcp_vllm_plugin_amd.varlen import VarlenLaunch
+
+    h, hkv, d, dtype = 14, 2, 128, torch.bfloat16
+    lens = [130, 1, 0, 77]
+    peers = [5, 16, 3, 41]  # local segment starts at token P of the request's frame
+    offs = [0, 0, 0, 20] if causal else [0, 0, 0, 0]
+    cache, bt, q, _ = _build(dev, layout, [L + o for L, o in zip(lens, offs)], peers, h, hkv,
+                             d, dtype, bs, seed=90 + bs)
+    cd, btd, qd = cache.to(dev), bt.to(dev), q[:sum(lens)].to(dev)
+    pc = PagedCache.from_tensor(cd)
+    ent, qs = [], 0
+    for r, (L, P, o) in enumerate(zip(lens, peers, offs)):
+        ent.append(make_entry(qs, L, segment_paged(pc, btd[r], P, L + o), o))
+        qs += L
+    launch = VarlenLaunch(ent, causal, True, dev)
+    scale = scale_for(d)
+    for rep in range(2):
+        if rep == 1:  # new cache contents, same addresses: the next run sees them
+            cd.copy_(torch.randn(cd.shape, generator=torch.Generator(device=dev).manual_seed(5),
+                                 device=dev).to(dtype))
+            cache = cd.cpu()
+        o_ = torch.zeros_like(qd)
+        lse_ = torch.full((h, qd.shape[0]), float("-inf"), device=dev)
+        launch.run(qd, o_, lse_, hkv, scale)
+        torch.cuda.synchronize()
+        qs = 0
+        for r, (L, P, o) in enumerate(zip(lens, peers, offs)):
+            kl, vl = orc.gather_paged(cache.float(), bt[r], P, L + o, layout)
+            ro, rl = orc.attn_with_lse(q[qs:qs + L].float(), kl, vl, scale,
+                                       o if causal else None)
+            assert max_err(o_[qs:qs + L], ro) <= OUT_TOL[dtype], (rep, r)
+            assert max_err(lse_[:, qs:qs + L], rl) <= LSE_TOL, (rep, r)
+            qs += L
+
+
+@pytest.mark.parametrize("bs", [1, 8, 32])
+def test_gather_paged_kv_bit_exact(dev, bs):
+    """hcp_gather_paged_kv == the oracle's gather (ring_backend.py:617-624)
+    bit for bit, both layouts' strides through one descriptor, head_dim 72 (a
+    row that is not a power of two of 16-byte chunks)."""
+    import numpy as np
+
+    from hcp_vllm_plugin_amd import _lib
+    from hcp_vllm_plugin_amd.varlen import ENTRY_DTYPE, _upload
+
+    for layout in ("v031", "v023"):
+        h, hkv, d, dtype = 4, 2, 72, torch.float16
+        lens, peers = [50, 0, 3, 200], [7, 0, 31, 16]
+        cache, bt, _, _ = _build(dev, layout, lens, peers, h, hkv, d, dtype, bs, seed=bs)
+        cd, btd = cache.to(dev), bt.to(dev)
+        pc = PagedCache.from_tensor(cd)
+        ent = [make_entry(0, 1, segment_paged(pc, btd[r], P, L), 0)
+               for r, (L, P) in enumerate(zip(lens, peers))]
+        arr = np.concatenate([np.frombuffer(e, dtype=ENTRY_DTYPE) for e in ent])
+        starts = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+        keep, (ep, sp) = _upload([arr, starts], dev)
+        k = torch.zeros(sum(lens), hkv, d, dtype=dtype, device=dev)
+        v = torch.zeros_like(k)
+        rc = _lib.lib().hcp_gather_paged_kv(ep, len(ent), sp, max(lens), hkv, d,
+                                           _lib.dtype_code(dtype), k.data_ptr(), v.data_ptr(),
+                                           _lib.stream_ptr(dev))
+        assert rc == 0, _lib.lib().hcp_last_error()
+        torch.cuda.synchronize()
+        for r, (L, P) in enumerate(zip(lens, peers)):
+            kr, vr = orc.gather_paged(cache, bt[r], P, L, layout)
+            s = int(starts[r])
+            assert torch.equal(k[s:s + L].cpu(), kr.to(dtype)), (layout, r)
+            assert torch.equal(v[s:s + L].cpu(), vr.to(dtype)), (layout, r)
