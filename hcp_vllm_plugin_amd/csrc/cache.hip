@@ -70,6 +70,8 @@ __global__ __launch_bounds__(256) void gather_segments_kernel(GatherParams p) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t row = p.cpr_shift >= 0 ? gid >> p.cpr_shift : gid / p.cpr;
   if (row >= s.len * p.num_kv_heads) return;
+  // only paged entries with a power-of-two block size are gathered
+  if (s.block_table == 0 || s.block_size <= 0 || (s.block_size & (s.block_size - 1))) return;
   const int ch = static_cast<int>(gid - row * p.cpr);
   const int64_t t = row / p.num_kv_heads;
   const int h = static_cast<int>(row - t * p.num_kv_heads);

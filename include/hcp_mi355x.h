@@ -428,7 +428,8 @@ int hcp_reshape_and_cache(const void* key, int64_t k_stride_tok,
  * kernel reads from one block (hcp_plan_varlen_tiles refuses those), and runs
  * the whole batch in one launch.  `entries` (paged: block_table != 0) and
  * `out_start` (int64) are DEVICE arrays; at most 65535 entries, none longer
- * than max_len.  Block ids at or past kv.num_blocks (when given) are clamped
+ * than max_len; an entry that is not paged or whose block_size is not a
+ * power of two is skipped (its rows are left as they were).  Block ids at or past kv.num_blocks (when given) are clamped
  * to the last block.  head_dim a multiple of 8 up to 256; k_out / v_out
  * 16-byte aligned.
  */
