@@ -211,6 +211,12 @@ int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries, 
     // the prefill kernel reads a wave's 16 rows of a paged tile from one block
     if (en.kv.block_table && (en.kv.stride_tok <= 0 || en.kv.stride_tok >= (int64_t{1} << 24)))
       return fail(HCP_EUNSUPPORTED, "%s: entry %d: paged token stride must be in (0, 2^24)", who, i);
+    if (!en.kv.block_table && en.kv.len > 1 &&
+        (en.kv.stride_tok <= 0 || en.kv.stride_tok >= (int64_t{1} << 24)))
+      return fail(HCP_EUNSUPPORTED, "%s: entry %d: token stride must be in (0, 2^24)", who, i);
+    if (en.kv.block_table && (en.kv.stride_block <= 0 || en.kv.stride_block >= (int64_t{1} << 31)))
+      return fail(HCP_EUNSUPPORTED, "%s: entry %d: block stride must be in (0, 2^31) elements",
+                  who, i);
     if (en.kv.block_table && en.kv.block_size < hcp::kFwdPagedMinBlock)
       return fail(HCP_EUNSUPPORTED, "%s: entry %d: paged prefill needs block_size >= %d, got %d",
                   who, i, hcp::kFwdPagedMinBlock, en.kv.block_size);

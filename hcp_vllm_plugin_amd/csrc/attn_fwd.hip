@@ -242,6 +242,7 @@ fa_fwd_kernel(FwdParams p) {
   };
   const int64_t rowb_g = e.kv.stride_tok * 2;  // bytes between tokens in HBM
   const uint32_t rowb32 = static_cast<uint32_t>(rowb_g);
+  const uint32_t tileb32 = static_cast<uint32_t>(BN) * rowb32;  // bytes of a tile's rows
   const char* kseg;
   const char* vseg;
   int bs_shift = 0, bs_mask = 0;
@@ -258,6 +259,7 @@ fa_fwd_kernel(FwdParams p) {
     kseg = reinterpret_cast<const char*>(e.kv.k_addr) + base;
     vseg = reinterpret_cast<const char*>(e.kv.v_addr) + base;
   }
+  const uint32_t blockb32 = static_cast<uint32_t>(blockb);  // under 4 GiB (checked on the host)
 
   // Per-lane 32-bit byte offsets (loop invariant) under a wave-uniform
   // descriptor, the SGPR-base + VGPR-offset form of buffer_load ... lds:
@@ -312,17 +314,21 @@ fa_fwd_kernel(FwdParams p) {
   // as zeros: unused cache slots may hold NaNs).  The rows start on a
   // multiple of 16 of the block frame (the segment start is aligned down to
   // 16 keys), so with block_size >= 16 all WROWS = 16 of them lie in the block.
+  // (32-bit offsets: a block spans under 4 GiB -- hcp_plan_varlen_tiles
+  // checks it -- so only the final address add is 64-bit, and the bounds are
+  // selects, not branches)
   auto page_rsrc = [&](const char* seg, uint32_t id, int t) __attribute__((always_inline)) {
     t = t < ntiles ? t : ntiles - 1;
     const int r0 = t * BN + wave * WROWS;
-    const int in_blk = static_cast<int>((e.kv.start + r0) & bs_mask);
+    const int in_blk = (static_cast<int>(e.kv.start) + r0) & bs_mask;
     int rows = kv_len - r0;
     rows = rows < WROWS ? rows : WROWS;
     rows = rows < e.kv.block_size - in_blk ? rows : e.kv.block_size - in_blk;
-    const int nrec = rows > 0 ? static_cast<int>((rows - 1) * rowb_g) + rowv : 0;
-    return __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(seg + static_cast<int64_t>(id) * blockb + in_blk * rowb_g), 0, nrec,
-        kBufferRsrcWord3);
+    const uint32_t nrec = rows > 0 ? static_cast<uint32_t>(rows - 1) * rowb32 + rowv : 0u;
+    const uint64_t off = static_cast<uint64_t>(id) * blockb32 +
+                         static_cast<uint32_t>(in_blk) * rowb32;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(seg + off), 0,
+                                             static_cast<int>(nrec), kBufferRsrcWord3);
   };
 
   // Contiguous prologue loads of one tile of K or V.  Ragged tiles clamp
@@ -356,14 +362,16 @@ fa_fwd_kernel(FwdParams p) {
   // nobody reads); a ragged last tile gets num_records = its valid bytes, so
   // rows past the segment read as zeros (they are masked in S, and zero V
   // rows meet P = 0) with no per-lane clamping.
+  // (a tile's rows span under 2^31 bytes: the token stride is below 2^24
+  // elements, checked on the host)
   auto tile_rsrc = [&](const char* seg, int tile_idx) __attribute__((always_inline)) {
     const int t = tile_idx < ntiles ? tile_idx : ntiles - 1;
     const int rows = kv_len - t * BN;
-    const int nrec = rows >= BN ? 0x7fffffff
-                                : static_cast<int>((rows - 1) * rowb_g) + rowv;
+    const uint32_t nrec =
+        rows >= BN ? 0x7fffffffu : static_cast<uint32_t>(rows - 1) * rowb32 + rowv;
     return __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(seg + static_cast<int64_t>(t) * BN * rowb_g), 0, nrec,
-        kBufferRsrcWord3);
+        const_cast<char*>(seg + static_cast<uint64_t>(static_cast<uint32_t>(t)) * tileb32), 0,
+        static_cast<int>(nrec), kBufferRsrcWord3);
   };
   auto load_at = [&](__amdgpu_buffer_rsrc_t rs, uint32_t o, int i, HCP_LDS(char)* dst)
       __attribute__((always_inline)) {
