@@ -217,6 +217,11 @@ int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries, 
     if (en.kv.block_table && (en.kv.stride_block <= 0 || en.kv.stride_block >= (int64_t{1} << 31)))
       return fail(HCP_EUNSUPPORTED, "%s: entry %d: block stride must be in (0, 2^31) elements",
                   who, i);
+    // the kernel's in-block byte offsets are 32-bit
+    if (en.kv.block_table &&
+        static_cast<int64_t>(en.kv.block_size) * en.kv.stride_tok * 2 > (int64_t{1} << 32))
+      return fail(HCP_EUNSUPPORTED, "%s: entry %d: block_size * token stride spans over 4 GiB",
+                  who, i);
     if (en.kv.block_table && en.kv.block_size < hcp::kFwdPagedMinBlock)
       return fail(HCP_EUNSUPPORTED, "%s: entry %d: paged prefill needs block_size >= %d, got %d",
                   who, i, hcp::kFwdPagedMinBlock, en.kv.block_size);

@@ -185,8 +185,10 @@ int hcp_varlen_block_m(int32_t head_dim, int32_t dtype);
  * `tiles_out`, heaviest tile first (longest-processing-time order), and
  * returns the number of tiles (or a negative status; HCP_EWORKSPACE if cap is
  * too small; HCP_EUNSUPPORTED for a paged entry with block_size < 16, since the
- * prefill kernel reads each 16-row share of a 64-key tile from one block).
- * Runs on the CPU only.
+ * prefill kernel reads each 16-row share of a 64-key tile from one block, and
+ * for strides its 32-bit tile offsets cannot address: a token stride of 2^24
+ * elements or more, a block stride of 2^31 elements or more, or block_size *
+ * token stride over 4 GiB).  Runs on the CPU only.
  */
 int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries,
                           int32_t causal, int32_t block_m, int32_t* tiles_out,

@@ -126,6 +126,29 @@ def test_plan_varlen_tiles_rejects_small_paged_blocks(L):
             assert b"block_size >= 16" in L.hcp_last_error()
 
 
+def test_plan_varlen_tiles_rejects_strides_beyond_32bit_offsets(L):
+    """The prefill kernel forms tile offsets in 32 bits: a contiguous token
+    stride of 2^24 elements or more, a block stride of 2^31 or more, or a
+    block whose rows span over 4 GiB is refused, not mis-addressed."""
+    def plan(**kv):
+        e = _entry(0, 100, 0, 300)
+        for k, v in kv.items():
+            setattr(e.kv, k, v)
+        arr = (VarlenEntry * 1)(e)
+        tiles = (ctypes.c_int32 * 8)()
+        return L.hcp_plan_varlen_tiles(arr, 1, 1, 128, tiles, 4)
+
+    assert plan() == 1
+    assert plan(stride_tok=1 << 24) == _lib.HCP_EUNSUPPORTED
+    paged = dict(block_table=0x2000, block_size=16, stride_block=16 * 1024, stride_tok=256)
+    assert plan(**paged) == 1
+    assert plan(**{**paged, "stride_block": 1 << 31}) == _lib.HCP_EUNSUPPORTED
+    # 256 rows at a 2^23-element (16 MiB) token stride: a block spans 4 GiB + 1 row
+    big = {**paged, "block_size": 256, "stride_tok": (1 << 23) + 8, "stride_block": 1 << 30}
+    assert plan(**big) == _lib.HCP_EUNSUPPORTED
+    assert b"4 GiB" in L.hcp_last_error()
+
+
 def test_plan_decode_splits_partition_each_segment(L):
     # 3 sequences: (kv lens of its entries)
     seqs = [[4096, 700], [0, 1], [33, 2048, 5]]
