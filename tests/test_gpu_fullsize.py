@@ -70,6 +70,39 @@ def test_ring_prefill_step_full_size(dev, h, hkv, n_q, n_loc, n_peer, q0, n_out,
         assert max_err(lse[:, r0:r0 + 16], rl) <= LSE_TOL, r0
 
 
+def test_ring_prefill_step_full_size_fp16(dev):
+    """The 7B 8k + 8k ring step in fp16 (the reference's probe dtype; gate
+    2e-3 on out): sampled rows against the oracle, and the whole output
+    against one causal pass over [peer; local]."""
+    h, hkv, d, n = 28, 4, 128, 8192
+    g = torch.Generator(device=dev).manual_seed(16)
+    ch = torch.randperm(d, generator=torch.Generator().manual_seed(16))[:4]
+
+    def draw(shape, outlier=False):
+        x = torch.randn(*shape, generator=g, device=dev)
+        if outlier:
+            x[..., ch] *= 8.0
+        return x.to(torch.float16)
+
+    q = draw((n, h, d))
+    kl, vl, kp, vp = draw((n, hkv, d), True), draw((n, hkv, d)), draw((n, hkv, d), True), draw((n, hkv, d))
+    scale = scale_for(d)
+    o_peer, lse_peer = ring_attn_with_lse(q, kp, vp, scale, None)
+    lse = torch.empty(h, n, dtype=torch.float32, device=dev)
+    out = ring_attn_merged(q, kl, vl, scale, 0, o_peer, lse_peer, output_lse=lse)
+    kk, vv = torch.cat([kp, kl]), torch.cat([vp, vl])
+    o1, l1 = ring_attn_with_lse(q, kk, vv, scale, n)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and torch.isfinite(out).all()
+    assert max_err(out, o1) <= 2 * OUT_TOL[torch.float16], max_err(out, o1)
+    assert max_err(lse, l1) <= 2 * LSE_TOL
+    kc, vc = kk.float().cpu(), vv.float().cpu()
+    for r0 in (0, 4100, 8176):
+        ro, rl = orc.attn_with_lse(q[r0:r0 + 16].float().cpu(), kc, vc, scale, n + r0)
+        assert max_err(out[r0:r0 + 16], ro) <= OUT_TOL[torch.float16], (r0, max_err(out[r0:r0 + 16], ro))
+        assert max_err(lse[:, r0:r0 + 16], rl) <= LSE_TOL, r0
+
+
 @pytest.mark.parametrize("peer_layout", ["head_major", "token_major"])
 def test_split_kv_decode_full_size(dev, peer_layout):
     """64 sequences, each 32768 contiguous peer keys + U[512, 2048] local keys
