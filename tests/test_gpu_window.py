@@ -62,13 +62,15 @@ def test_window_d64_fp16_and_noncausal_ignores_it(dev):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
+@pytest.mark.parametrize("bs", [16, 4])
 @pytest.mark.parametrize("layout", ["v031", "v023"])
 @pytest.mark.parametrize("w", [1, 50, 333])
-def test_window_varlen_paged(dev, layout, w):
+def test_window_varlen_paged(dev, layout, w, bs):
     """Several requests over the paged cache in one causal launch, each with
-    its own offset (and a segment starting mid-block), one window."""
+    its own offset (and a segment starting mid-block), one window; block
+    size 4 runs through the device gather."""
     gen = torch.Generator().manual_seed(40 + w)
-    h, hkv, d, bs = 28, 4, 128, 16
+    h, hkv, d = 28, 4, 128
     reqs = [(300, 300, 0), (17, 517, 0), (129, 1000, 200), (64, 64, 0), (200, 900, 0)]
     nb = sum(-(-(s + tk) // bs) for _, tk, s in reqs) + 2
     cache = randn(gen, (nb, hkv, bs, 2 * d) if layout == "v031" else (nb, 2, bs, hkv, d),
