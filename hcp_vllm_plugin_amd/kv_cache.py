@@ -23,18 +23,44 @@ from .varlen import PagedCache
 
 __all__ = ["reshape_and_cache"]
 
+# Cache descriptors by (address, shape, strides, dtype): the write runs once per
+# layer and step, and building the descriptor each time was a third of its
+# host cost.  The key fixes every field the descriptor holds, so a descriptor
+# found here is the one the tensor would produce.
+_DESCS: dict = {}
+_MAX_DESCS = 1024
+
+
+def _cache_desc(kv_cache: torch.Tensor):
+    ck = (kv_cache.data_ptr(), tuple(kv_cache.shape), kv_cache.stride(), kv_cache.dtype)
+    ent = _DESCS.get(ck)
+    if ent is None:
+        pc = PagedCache.from_tensor(kv_cache)
+        desc = _lib.PagedCacheDesc()
+        desc.k_addr = pc.k_addr
+        desc.v_addr = pc.v_addr
+        desc.stride_block = pc.stride_block
+        desc.stride_head = pc.stride_head
+        desc.stride_tok = pc.stride_tok
+        desc.num_blocks = kv_cache.shape[0]
+        desc.block_size = pc.block_size
+        if len(_DESCS) >= _MAX_DESCS:
+            _DESCS.clear()
+        ent = _DESCS[ck] = (desc, ctypes.addressof(desc), pc.num_kv_heads, pc.head_dim)
+    return ent
+
 
 def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                       slot_mapping: torch.Tensor) -> None:
     """Write ``key``/``value`` ``[N, Hkv, D]`` rows ``[0, n)``, ``n =
     slot_mapping.numel()``, into ``kv_cache`` at ``slot_mapping``."""
-    pc = PagedCache.from_tensor(kv_cache)
+    _, desc_addr, hkv, d = _cache_desc(kv_cache)
     n = slot_mapping.numel()
     if key.shape != value.shape or key.dim() != 3:
         raise ValueError("key/value must be [N, Hkv, D] of one shape")
     if key.shape[0] < n:
         raise ValueError(f"{n} slots for {key.shape[0]} key rows")
-    if key.shape[1] != pc.num_kv_heads or key.shape[2] != pc.head_dim:
+    if key.shape[1] != hkv or key.shape[2] != d:
         raise ValueError("key/value heads or head_dim do not match the cache")
     if key.dtype != kv_cache.dtype or value.dtype != kv_cache.dtype:
         raise ValueError("key/value dtype must match the cache dtype")
@@ -45,22 +71,15 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Te
     if n == 0:
         return
     slots = slot_mapping.contiguous()
-    desc = _lib.PagedCacheDesc()
-    desc.k_addr = pc.k_addr
-    desc.v_addr = pc.v_addr
-    desc.stride_block = pc.stride_block
-    desc.stride_head = pc.stride_head
-    desc.stride_tok = pc.stride_tok
-    desc.num_blocks = kv_cache.shape[0]
-    desc.block_size = pc.block_size
     L = _lib.lib()
-    with torch.cuda.device(key.device):
-        rc = L.hcp_reshape_and_cache(
-            key.data_ptr(), key.stride(0), key.stride(1),
+    args = (key.data_ptr(), key.stride(0), key.stride(1),
             value.data_ptr(), value.stride(0), value.stride(1),
-            slots.data_ptr(),
-            _lib.DTYPE_I64 if slots.dtype == torch.int64 else _lib.DTYPE_I32,
-            n, pc.num_kv_heads, pc.head_dim, ctypes.byref(desc),
-            _lib.dtype_code(key.dtype), _lib.stream_ptr(key.device),
-        )
+            slots.data_ptr(), _lib.DTYPE_I64 if slots.dtype == torch.int64 else _lib.DTYPE_I32,
+            n, hkv, d, desc_addr, _lib.dtype_code(key.dtype))
+    dev = key.device
+    if dev.index == torch.cuda.current_device():
+        rc = L.hcp_reshape_and_cache(*args, torch.cuda.current_stream(dev).cuda_stream)
+    else:
+        with torch.cuda.device(dev):
+            rc = L.hcp_reshape_and_cache(*args, _lib.stream_ptr(dev))
     _lib.check(rc, "hcp_reshape_and_cache")
