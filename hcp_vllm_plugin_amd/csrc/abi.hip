@@ -122,6 +122,8 @@ static int fwd_lse_impl(const char* who, const void* q, const void* k, const voi
   if (!(scale > 0.f) || !std::isfinite(scale))
     return fail(HCP_EINVAL, "%s: scale must be finite and > 0", who);
   if (tq > (int64_t)INT32_MAX * 64) return fail(HCP_EINVAL, "%s: tq too large", who);
+  // the kernel counts a segment's keys (and its tiles' key offsets) in int32
+  if (tk > (int64_t)INT32_MAX - 256) return fail(HCP_EUNSUPPORTED, "%s: tk too large", who);
   if (window < 0) return fail(HCP_EINVAL, "%s: negative window", who);
 
   hcp::FwdParams p{};
@@ -150,8 +152,10 @@ static int fwd_lse_impl(const char* who, const void* q, const void* k, const voi
   p.single.kv.len = tk;
   if (k_stride_tok != v_stride_tok || k_stride_head != v_stride_head)
     return fail(HCP_EUNSUPPORTED, "%s: k and v must share strides", who);
-  if (k_stride_tok <= 0 || k_stride_tok >= (int64_t{1} << 24))
-    return fail(HCP_EUNSUPPORTED, "%s: k token stride must be in (0, 2^24) elements", who);
+  // the kernel's tile offsets are 32-bit: 64 rows of a tile span under 2^31
+  // bytes (a single key row is never stepped over)
+  if (tk > 1 && (k_stride_tok <= 0 || k_stride_tok >= (int64_t{1} << 24)))
+    return fail(HCP_EUNSUPPORTED, "%s: k/v token stride must be in (0, 2^24) elements", who);
   set_acc(p, acc);
   hipError_t e = hcp::launch_fwd(p, head_dim, dtype, causal != 0, false, false,
                                  static_cast<hipStream_t>(stream));
@@ -208,6 +212,9 @@ int hcp_plan_varlen_tiles(const hcp_varlen_entry* entries, int32_t num_entries, 
   for (int32_t i = 0; i < num_entries; ++i) {
     const hcp_varlen_entry& en = entries[i];
     if (en.q_len < 0 || en.kv.len < 0) return fail(HCP_EINVAL, "%s: entry %d negative", who, i);
+    // the kernel counts a segment's keys (and its tiles' key offsets) in int32
+    if (en.kv.len > (int64_t)INT32_MAX - 256)
+      return fail(HCP_EUNSUPPORTED, "%s: entry %d: kv len too large", who, i);
     // the prefill kernel reads a wave's 16 rows of a paged tile from one block
     if (en.kv.block_table && (en.kv.stride_tok <= 0 || en.kv.stride_tok >= (int64_t{1} << 24)))
       return fail(HCP_EUNSUPPORTED, "%s: entry %d: paged token stride must be in (0, 2^24)", who, i);
@@ -670,8 +677,11 @@ int hcp_gather_paged_kv(const hcp_varlen_entry* entries, int32_t num_entries,
   if (!entries || !out_start || !k_out || !v_out) return fail(HCP_EINVAL, "%s: null pointer", who);
   if (!aligned8(entries) || !aligned8(out_start) || !aligned16(k_out) || !aligned16(v_out))
     return fail(HCP_EINVAL, "%s: misaligned pointer", who);
-  if (max_len * num_kv_heads > (int64_t)INT32_MAX * 16)
-    return fail(HCP_EINVAL, "%s: too many rows", who);
+  // one thread per 16-byte piece of a (token, head) row, 256 per workgroup:
+  // the launch's grid.x (and grid.x * 256) must stay within 32 bits
+  if (max_len * num_kv_heads * (head_dim / 8) > (int64_t{1} << 32) - 256)
+    return fail(HCP_EINVAL, "%s: too many rows (max_len * num_kv_heads * head_dim / 8 >= 2^32)",
+                who);
   hcp::GatherParams p{};
   p.entries = entries;
   p.out_start = out_start;

@@ -97,6 +97,16 @@ __device__ __forceinline__ int tile_swz(int row) {
   return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
 }
 
+// The lane's index in its wave, read afresh: an opaque read the compiler
+// cannot merge with an earlier one, so a value derived from it is rebuilt
+// where it is used instead of being held in a register across the tile loop
+// (which needs every register).
+__device__ __forceinline__ int lane_id_fresh() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 template <typename V8>
 __device__ __forceinline__ V8 lds_read16(const HCP_LDS(char)* p) {
   return __builtin_bit_cast(V8, *reinterpret_cast<const HCP_LDS(u32x4)*>(p));
@@ -288,7 +298,7 @@ fa_fwd_kernel(FwdParams p) {
   auto load_ids = [&](int t0) __attribute__((always_inline)) {
     uint32_t id = 0;
     if constexpr (PAGED) {
-      int t = t0 + lane;
+      int t = t0 + lane_id_fresh();
       t = t < ntiles ? t : ntiles - 1;
       int key = t * BN + wave * WROWS;
       key = key < kv_len ? key : kv_len - 1;
@@ -385,26 +395,51 @@ fa_fwd_kernel(FwdParams p) {
   constexpr int kLoadEvery = 4;
 
   // ---- LDS read addresses (loop invariant, per lane) ----
+  // The swizzle permutes the 16 slots of each 256-byte group of a row only,
+  // so a slot 16 or more is the offset of slot - 16 plus 256 bytes: eight K
+  // and four V offsets per half cover any D (D = 256 rows have 32 slots).
   // K (A operand of S^T): row 32*blk + r32, 16-byte chunk 2s+g
   // (row + 32 has the same swizzle, so block 1 is an immediate offset)
+  // D = 256 (one wave per SIMD, every register in use): each offset is the
+  // first one XOR a constant, formed where it is used -- the row's slot
+  // bits (4..8) are disjoint from the row's own offset, so offset(s) =
+  // offset(0) ^ 32 s for K and offset(db) = offset(0) ^ 64 db for V -- by an
+  // opaque XOR the compiler cannot hoist into a loop-long register.
+  constexpr bool kXorOfs = D == 256;
+  auto xor_ofs = [&](int base, int c) __attribute__((always_inline)) {
+    if (c == 0) return base;
+    int r;
+    asm volatile("v_xor_b32 %0, %2, %1" : "=v"(r) : "v"(base), "n"(c));
+    return r;
+  };
+  constexpr int KO = kXorOfs ? 1 : (KSTEPS < 8 ? KSTEPS : 8);
   const int kx = tile_swz<D>(r32);
-  int koff[KSTEPS];
+  int koff[KO];
 #pragma unroll
-  for (int s = 0; s < KSTEPS; ++s) koff[s] = r32 * ROWB + (((2 * s + g) ^ kx) * 16);
+  for (int s = 0; s < KO; ++s) koff[s] = r32 * ROWB + (((2 * s + g) ^ kx) * 16);
+  auto kofs = [&](int s) __attribute__((always_inline)) {
+    if constexpr (kXorOfs) return xor_ofs(koff[0], 32 * s);
+    return koff[s % KO] + 256 * (s / KO);
+  };
   // V (transposing read): block beta = lane/16, i = lane%16 = 4*ee + aa reads
   // key 16t + 8h + 4*vg + ee, columns dblk*32 + 16*(beta&1) + 4*aa .. +3; the
   // swizzle of that key does not depend on t, so t is an immediate offset
   const int beta = lane >> 4, ee = (lane & 15) >> 2, aa = lane & 3;
   const int vg = beta >> 1;
   const int vs0 = 2 * (beta & 1) + (aa >> 1);
-  int voff[DBLK][2];
+  constexpr int VO = kXorOfs ? 1 : (DBLK < 4 ? DBLK : 4);
+  int voff[VO][2];
 #pragma unroll
-  for (int db = 0; db < DBLK; ++db)
+  for (int db = 0; db < VO; ++db)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int key = 8 * h + 4 * vg + ee;
       voff[db][h] = key * ROWB + (((4 * db + vs0) ^ tile_swz<D>(key)) * 16) + (aa & 1) * 8;
     }
+  auto vofs = [&](int db, int h) __attribute__((always_inline)) {
+    if constexpr (kXorOfs) return xor_ofs(voff[0][h], 64 * db);
+    return voff[db % VO][h] + 256 * (db / VO);
+  };
 
   // ---- online softmax state ----
   // m_ref: exponent reference of the row (log2 units), the row max of the
@@ -436,30 +471,51 @@ fa_fwd_kernel(FwdParams p) {
     S[1] = f32x16{};
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-      S[0] = E::mfma32(lds_read16<V8>(Ks + koff[s]), qf[s], S[0]);
-      S[1] = E::mfma32(lds_read16<V8>(Ks + koff[s] + 32 * ROWB), qf[s], S[1]);
+      S[0] = E::mfma32(lds_read16<V8>(Ks + kofs(s)), qf[s], S[0]);
+      S[1] = E::mfma32(lds_read16<V8>(Ks + kofs(s) + 32 * ROWB), qf[s], S[1]);
     }
   };
 
   // causal diagonal / ragged masking of tile n (keys n*BN ..): -inf
   // (and, with a window, tiles below some row's lower bound: the wave's last
-  // row has the highest bound off + wave_q0 + 32 - window)
+  // row has the highest bound off + wave_q0 + 32 - window).  The bounds are
+  // taken once, clamped into 32 bits around the segment's key range [0,
+  // kv_len): a tile's key offsets n*BN then compare against them directly.
+  auto clamp32 = [&](int64_t x) __attribute__((always_inline)) {
+    const int64_t lo = -BN, hi = static_cast<int64_t>(kv_len) + BN;
+    return static_cast<int>(x < lo ? lo : (x > hi ? hi : x));
+  };
+  // wave-uniform: a tile at n0 crosses the wave's causal diagonal when
+  // n0 > diag_from, lies (partly) below its window when n0 < win_below
+  const int diag_from = CAUSAL ? clamp32(off + wave_q0 - BN + 1) : 0;
+  const int win_below = win > 0 ? clamp32(off + wave_q0 + 32 - win) : 0;
   auto needs_mask = [&](int n) __attribute__((always_inline)) {
     const int n0 = n * BN;
-    return (n0 + BN > kv_len) || (CAUSAL && (n0 + BN - 1 > off + wave_q0)) ||
-           (win > 0 && n0 < off + wave_q0 + 32 - win) || (PAGED && n0 < lead);
+    return (n0 + BN > kv_len) || (CAUSAL && n0 > diag_from) || (win > 0 && n0 < win_below) ||
+           (PAGED && n0 < lead);
+  };
+  // a wave-uniform bound b relative to a tile, clamped so that b + r32 (the
+  // lane's row) stays exact wherever it lies in [-1, BN] and saturates
+  // outside it; scalar 64-bit arithmetic, one 32-bit add per lane
+  auto rel = [&](int64_t b) __attribute__((always_inline)) {
+    const int64_t lo = -BN - 32, hi = BN;
+    return static_cast<int>(b < lo ? lo : (b > hi ? hi : b)) + r32;
   };
   auto apply_mask = [&](f32x16 (&S)[2], int n) __attribute__((always_inline)) {
     const int n0 = n * BN;
     const int lim_r = kv_len - 1 - n0;
-    const int64_t lim_c64 = CAUSAL ? off + qi - n0 : static_cast<int64_t>(BN);
-    const int lim_c = lim_c64 < BN ? static_cast<int>(lim_c64 < -1 ? -1 : lim_c64) : BN;
+    // last key the lane's row sees, relative to the tile: off + qi - n0
+    int lim_c = BN;
+    if (CAUSAL) {
+      lim_c = rel(off + wave_q0 - n0);
+      lim_c = lim_c < -1 ? -1 : (lim_c > BN ? BN : lim_c);
+    }
     const int lim = lim_r < lim_c ? lim_r : lim_c;
     // lowest visible key of the lane's row, relative to the tile (the window's
-    // bound, and the paged alignment lead)
-    int64_t lo64 = win > 0 ? off + qi - win + 1 - n0 : 0;
-    if (PAGED && lead - n0 > lo64) lo64 = lead - n0;
-    const int lo = lo64 > 0 ? (lo64 < BN ? static_cast<int>(lo64) : BN) : 0;
+    // bound off + qi - window + 1, and the paged alignment lead)
+    int lo = win > 0 ? rel(off + wave_q0 - win + 1 - n0) : 0;
+    if (PAGED && lead - n0 > lo) lo = lead - n0;
+    lo = lo < 0 ? 0 : (lo > BN ? BN : lo);
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -525,8 +581,8 @@ fa_fwd_kernel(FwdParams p) {
   constexpr int VR = HCP_VPF + 1;  // V fragment ring
   auto vread_at = [&](const HCP_LDS(char)* Vs, int j) __attribute__((always_inline)) {
     const int t = j / DBLK, db = j % DBLK;
-    const i16x4 lo = lds_read_tr(Vs + voff[db][0] + (16 * t) * ROWB);
-    const i16x4 hi = lds_read_tr(Vs + voff[db][1] + (16 * t) * ROWB);
+    const i16x4 lo = lds_read_tr(Vs + vofs(db, 0) + (16 * t) * ROWB);
+    const i16x4 hi = lds_read_tr(Vs + vofs(db, 1) + (16 * t) * ROWB);
     u32x4 w;
     w[0] = __builtin_bit_cast(u32x2, lo)[0];
     w[1] = __builtin_bit_cast(u32x2, lo)[1];
@@ -578,13 +634,13 @@ fa_fwd_kernel(FwdParams p) {
     V8 kf[KR];
 #pragma unroll
     for (int j = 0; j < HCP_KPF; ++j)
-      kf[j] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
+      kf[j] = lds_read16<V8>(Ks + kofs(j >> 1) + (j & 1) * 32 * ROWB);
 #pragma unroll
     for (int st = 0; st < NA; ++st) {
       const int s = st >> 1, blk = st & 1;
       if (st + HCP_KPF < NA) {
         const int j = st + HCP_KPF;
-        kf[j % KR] = lds_read16<V8>(Ks + koff[j >> 1] + (j & 1) * 32 * ROWB);
+        kf[j % KR] = lds_read16<V8>(Ks + kofs(j >> 1) + (j & 1) * 32 * ROWB);
       }
       Sn[blk] = E::mfma32(kf[st % KR], qf[s], s == 0 ? f32x16{} : Sn[blk]);
       // K(n+2) and V(n+1) tile loads, alternating, one every kLoadEvery/2
@@ -735,6 +791,11 @@ fa_fwd_kernel(FwdParams p) {
   // ---- epilogue ----
   // (AGPR accumulator: the last products have landed before it is read)
   acc_fence();
+  // (the lane-dependent values of the epilogue are rebuilt from a fresh
+  // lane id rather than held across the tile loop)
+  const int lane_e = lane_id_fresh();
+  const int r32e = lane_e & 31, ge = lane_e >> 5;
+  const int64_t qi_e = wave_q0 + r32e;
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float lr_tot = lr_run + __shfl_xor(lr_run, 32);
   // Merge path: this wave's 32 rows of the partial state are fetched whole
@@ -760,16 +821,16 @@ fa_fwd_kernel(FwdParams p) {
         const_cast<char*>(abase), 0, static_cast<int>((rows - 1) * sb) + rowv, kBufferRsrcWord3);
 #pragma unroll
     for (int i = 0; i < 32 / RPL; ++i) {
-      const int r = i * RPL + lane / CPR;
-      const int lc = (lane % CPR) ^ (r & (CPR - 1));
+      const int r = i * RPL + lane_e / CPR;
+      const int lc = (lane_e % CPR) ^ (r & (CPR - 1));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rs, reinterpret_cast<HCP_LDS(void)*>(abuf + i * 1024), 16,
           lc * 8 < dv ? static_cast<int>(r * sb) + lc * 16 : static_cast<int>(kOob), 0, 0, 0);
     }
   }
-  if (q_valid) {
+  if (qi_e < q_len) {
     const float inv = lr_tot > 0.f ? 1.f / lr_tot : 0.f;
-    const int64_t row = e.q_start + qi;
+    const int64_t row = e.q_start + qi_e;
     char* orow = reinterpret_cast<char*>(p.out) +
                  (row * p.o_stride_tok + static_cast<int64_t>(head) * p.o_stride_head) * 2;
     float lse_row = l_tot > 0.f ? m_ref * kLn2 + __logf(l_tot) : -INFINITY;
@@ -778,7 +839,7 @@ fa_fwd_kernel(FwdParams p) {
       for (int db = 0; db < DBLK; ++db) {
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-          const int d0 = 32 * db + 8 * a + 4 * g;
+          const int d0 = 32 * db + 8 * a + 4 * ge;
           u32x2 w;
           w[0] = pack2<T>(oacc[db][4 * a + 0] * inv, oacc[db][4 * a + 1] * inv);
           w[1] = pack2<T>(oacc[db][4 * a + 2] * inv, oacc[db][4 * a + 3] * inv);
@@ -813,14 +874,14 @@ fa_fwd_kernel(FwdParams p) {
       for (int db = 0; db < DBLK; ++db) {
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-          const int d0 = 32 * db + 8 * a + 4 * g;
+          const int d0 = 32 * db + 8 * a + 4 * ge;
           u32x2 own;
           own[0] = pack2<T>(oacc[db][4 * a + 0] * inv, oacc[db][4 * a + 1] * inv);
           own[1] = pack2<T>(oacc[db][4 * a + 2] * inv, oacc[db][4 * a + 3] * inv);
           if (!(w_own > 0.f)) own = u32x2{0, 0};
           const u32x2 oth =
               w_acc > 0.f ? *reinterpret_cast<const HCP_LDS(u32x2)*>(
-                                abuf + r32 * ROWB + (((4 * db + a) ^ (r32 & (CPR - 1))) * 16) + 8 * g)
+                                abuf + r32e * ROWB + (((4 * db + a) ^ (r32e & (CPR - 1))) * 16) + 8 * ge)
                           : u32x2{0, 0};
           const u32x2 pre = acc_pre ? oth : own, suf = acc_pre ? own : oth;
           u32x2 w;
@@ -836,7 +897,7 @@ fa_fwd_kernel(FwdParams p) {
         }
       }
     }
-    if (g == 0 && p.lse != nullptr) p.lse[static_cast<int64_t>(head) * p.lse_stride_head + row] = lse_row;
+    if (ge == 0 && p.lse != nullptr) p.lse[static_cast<int64_t>(head) * p.lse_stride_head + row] = lse_row;
   }
 }
 

@@ -40,6 +40,11 @@ Drop-in for hcp_vllm_plugin/ring_backend.py's hot path:
   local pass counts as one); the legacy keys ``attn_triton`` /
   ``merge_triton`` mirror them so validators that read those names still see
   which path ran, and ``attn_torch`` / ``merge_torch`` stay 0.
+* The validators' other evidence (ring_backend.py:228-275, :790-810), same
+  names and meaning: ``STAGING_STATS`` / ``reset_staging_stats`` (staging
+  high-water marks), ``WRITE_TRACK`` / ``reset_write_tracking`` (pool slots
+  written, the chunk-A ``overlap`` probe in ``forward``, decode-ring
+  ``skipped`` writes) and ``BATCH_STATS`` / ``reset_batch_stats``.
 """
 
 from __future__ import annotations
@@ -103,6 +108,13 @@ PEER_REQ_MAP: dict[int, list[str]] = {}
 # streams already ordered after it); a forward on any stream waits on the
 # event once before reading the chunk
 _STAGE_READY: dict[tuple[str, str], tuple[torch.cuda.Event, set]] = {}
+# Bumped whenever a chunk key appears in or leaves the staging dict, or the
+# request map changes: which requests take which chunks (the decode-step
+# template) is decided from these, and stays valid while the count holds.
+# (A further layer of an already staged chunk does not bump it; each layer's
+# lookup checks its own entry.)
+_STAGE_GEN = [0]
+_CHUNK_LAYERS: dict[str, int] = {}  # chunk key -> layers staged
 
 
 def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Tensor,
@@ -126,6 +138,10 @@ def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Ten
     if on_gpu and ready is not None:
         torch.cuda.current_stream(k.device).wait_event(ready)
     key = (chunk_key, layer_name)
+    if key not in PEER_KV_STAGING:
+        _CHUNK_LAYERS[chunk_key] = _CHUNK_LAYERS.get(chunk_key, 0) + 1
+        if _CHUNK_LAYERS[chunk_key] == 1:
+            _STAGE_GEN[0] += 1
     PEER_KV_STAGING[key] = (head_major(k), head_major(v))
     if on_gpu:
         st = torch.cuda.current_stream(k.device)
@@ -134,6 +150,29 @@ def stage_peer_kv(chunk_key: str, layer_name: str, k: torch.Tensor, v: torch.Ten
         _STAGE_READY[key] = (ev, {st})
     else:
         _STAGE_READY.pop(key, None)
+    _note_staging(k)
+
+
+# High-water marks of the staging dict (ring_backend.py:228-251): staging is
+# freed when a request finishes, so post-run checks read these instead.
+STAGING_STATS: dict = {"max_concurrent_chunks": 0, "max_staged_layers": 0, "last_chunk_len": 0}
+
+
+def reset_staging_stats() -> None:
+    STAGING_STATS["max_concurrent_chunks"] = 0
+    STAGING_STATS["max_staged_layers"] = 0
+    STAGING_STATS["last_chunk_len"] = 0
+
+
+def _note_staging(k: torch.Tensor) -> None:
+    """Raise the high-water marks after a stage: (chunk, layer) entries held,
+    distinct chunks held, and the token count of the chunk just staged."""
+    STAGING_STATS["max_staged_layers"] = max(STAGING_STATS["max_staged_layers"],
+                                             len(PEER_KV_STAGING))
+    chunks = {key[0] for key in PEER_KV_STAGING}
+    STAGING_STATS["max_concurrent_chunks"] = max(STAGING_STATS["max_concurrent_chunks"],
+                                                 len(chunks))
+    STAGING_STATS["last_chunk_len"] = int(k.shape[0])
 
 
 def _wait_staged(key: tuple[str, str], kv: tuple[torch.Tensor, torch.Tensor]) -> None:
@@ -159,6 +198,8 @@ def drop_chunk_kv(chunk_key: str) -> int:
     for key in keys:
         del PEER_KV_STAGING[key]
         _STAGE_READY.pop(key, None)
+    if _CHUNK_LAYERS.pop(chunk_key, None) is not None:
+        _STAGE_GEN[0] += 1
     return len(keys)
 
 
@@ -166,11 +207,15 @@ def map_request_peer(first_block_id: int, chunk_keys) -> None:
     """Bind a request (by its first block id) to its ordered prefix chunks."""
     if isinstance(chunk_keys, str):
         chunk_keys = [chunk_keys]
-    PEER_REQ_MAP[first_block_id] = list(chunk_keys)
+    chunk_keys = list(chunk_keys)
+    if PEER_REQ_MAP.get(first_block_id) != chunk_keys:
+        PEER_REQ_MAP[first_block_id] = chunk_keys
+        _STAGE_GEN[0] += 1
 
 
 def unmap_request_peer(first_block_id: int) -> None:
-    PEER_REQ_MAP.pop(first_block_id, None)
+    if PEER_REQ_MAP.pop(first_block_id, None) is not None:
+        _STAGE_GEN[0] += 1
 
 
 def request_peer_chunk(first_block_id: int) -> list[str] | None:
@@ -181,6 +226,8 @@ def clear_peer_kv() -> None:
     PEER_KV_STAGING.clear()
     PEER_REQ_MAP.clear()
     _STAGE_READY.clear()
+    _CHUNK_LAYERS.clear()
+    _STAGE_GEN[0] += 1
 
 
 # ---------------------------------------------------------------------------
@@ -300,14 +347,38 @@ def _forward_attn_metadata(layer):
     return raw
 
 
-# Pool-write evidence (ring_backend.py:260-267): decode-ring tokens skipped.
-WRITE_TRACK: dict = {"enabled": False, "slots": set(), "skipped": 0}
+# Pool-write evidence (ring_backend.py:254-267), validation only.  While
+# enabled, do_kv_cache_update records the pool slots this worker wrote, and
+# forward counts in "overlap" every slot of a request's peer (chunk-A) region
+# among them: a memory-splitting worker never writes one.  "skipped" counts
+# decode-ring tokens whose pool write was skipped (always counted).
+WRITE_TRACK: dict = {"enabled": False, "slots": set(), "overlap": 0, "skipped": 0}
 
 
-def enable_write_tracking() -> None:
+def reset_write_tracking() -> None:
+    """Enable write tracking and clear its evidence (ring_backend.py:260-265)."""
     WRITE_TRACK["enabled"] = True
     WRITE_TRACK["slots"] = set()
+    WRITE_TRACK["overlap"] = 0
     WRITE_TRACK["skipped"] = 0
+
+
+enable_write_tracking = reset_write_tracking  # earlier name of the same call
+
+
+def _probe_chunk_a_writes(block_row: torch.Tensor, peer_end: int, block_size: int) -> int:
+    """Slots of the first ``peer_end`` positions of a request (its peer region,
+    through its block-table row) that this worker wrote; added to
+    ``WRITE_TRACK["overlap"]`` with a warning (ring_backend.py:790-810)."""
+    nb_a = (peer_end + block_size - 1) // block_size
+    blocks = block_row[:nb_a].tolist()
+    slots = [b * block_size + o for b in blocks for o in range(block_size)][:peer_end]
+    overlap = WRITE_TRACK["slots"].intersection(slots)
+    if overlap:
+        WRITE_TRACK["overlap"] += len(overlap)
+        logger.warning("HCP ring: %d chunk-A pool slots were written locally "
+                       "(expected 0 in a memory-splitting worker)", len(overlap))
+    return len(overlap)
 
 
 # ---------------------------------------------------------------------------
@@ -530,8 +601,10 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
                 and qsl[r] < slot_mapping.shape[0]}
 
     # -- planning -------------------------------------------------------------
-    def _peer_for_request(self, first_block: int, layer_name: str, n_reqs: int):
-        """Ordered staged (k, v) chunks of a request, or None (ring_backend.py:738-772)."""
+    def _peer_for_request(self, first_block: int, layer_name: str, n_reqs: int,
+                          probe: bool = False):
+        """Ordered staged (k, v) chunks of a request, or None (ring_backend.py:738-772).
+        ``probe``: only look (no warning, no stream ordering)."""
         ck_list = PEER_REQ_MAP.get(first_block)
         if ck_list is None and n_reqs == 1:
             chunks = {key[0] for key in PEER_KV_STAGING}
@@ -543,14 +616,37 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         for ck in ck_list:
             kv = PEER_KV_STAGING.get((ck, layer_name))
             if kv is None:
-                logger.warning(
-                    "HCP ring: request mapped to chunks %s but staging incomplete at layer %s; "
-                    "falling back to local path", ck_list, layer_name)
+                if not probe:
+                    logger.warning(
+                        "HCP ring: request mapped to chunks %s but staging incomplete at "
+                        "layer %s; falling back to local path", ck_list, layer_name)
                 return None
             parts.append(kv)
-        for ck, kv in zip(ck_list, parts):
-            _wait_staged((ck, layer_name), kv)
+        if not probe:
+            for ck, kv in zip(ck_list, parts):
+                _wait_staged((ck, layer_name), kv)
         return parts
+
+    def _write_probe(self, layer_name, qsl, seq_lens, block_table, first_blocks, pc,
+                     ring_on: bool, split: int) -> None:
+        """With write tracking on: every request that takes the ring path
+        (a peer region of ``peer_end > 0`` positions, from staged chunks or the
+        split env; decode-ring rows excepted) has its peer region's pool slots
+        checked against the slots this worker wrote (ring_backend.py:790-810)."""
+        ring_rows = _decode_ring_enabled() and bool(DECODE_RING_MAP)
+        n = len(seq_lens)
+        for r in range(n):
+            tq, tk = qsl[r + 1] - qsl[r], int(seq_lens[r])
+            if tq == 0 or (ring_rows and tq == 1 and first_blocks[r] in DECODE_RING_MAP):
+                continue
+            staged = (self._peer_for_request(first_blocks[r], layer_name, n, probe=True)
+                      if ring_on else None)
+            if staged is not None:
+                peer_end = min(sum(int(kv[0].shape[0]) for kv in staged), tk)
+            else:
+                peer_end = min(split, tk) if split > 0 else 0
+            if peer_end > 0:
+                _probe_chunk_a_writes(block_table[r], peer_end, pc.block_size)
 
     def _plan(self, layer_name, qsl, seq_lens, block_table, first_blocks, pc, split):
         plan = _Plan()
@@ -639,6 +735,9 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         if self._peer_free(ring_on, split, first_blocks, n):
             self._forward_local_only(query, out, qsl, seq_lens, block_table, pc, kv_cache)
             return output
+        if WRITE_TRACK["enabled"]:
+            self._write_probe(layer_name, qsl, seq_lens, block_table, first_blocks, pc,
+                              ring_on, split)
 
         is_decode = n > 0 and qsl == list(range(n + 1))
         if is_decode and self._forward_decode_staged(query, out, seq_lens, block_table,
@@ -803,8 +902,12 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
         if split > 0 or (_decode_ring_enabled() and DECODE_RING_MAP
                          and any(fb in DECODE_RING_MAP for fb in first_blocks)):
             return False
+        # (the staging generation: a chunk staged, dropped or mapped after the
+        # template was built -- even for a request the template saw without
+        # peers -- makes the next layer build a new one)
         key = ("dec_staged", self.sliding_window, pc.layout, pc.stride_tok, pc.stride_head,
-               pc.stride_block, pc.block_size, pc.num_blocks, pc.v_addr - pc.k_addr, ring_on)
+               pc.stride_block, pc.block_size, pc.num_blocks, pc.v_addr - pc.k_addr, ring_on,
+               _STAGE_GEN[0])
         st = _STEP["fast"].get(key)
         if st is None:
             st = self._decode_staged_template(seq_lens, block_table, first_blocks, pc, layer_name)

@@ -342,7 +342,7 @@ class VarlenLaunch:
                 cont["start"] = out_start
                 self._gather = {"paged": host, "out_start": out_start, "cont": cont,
                                 "total": int(lens.sum()), "max_len": int(lens.max()),
-                                "shape": None}
+                                "bufs": {}}
                 arr = cont
                 self.paged = False
         tiles = (ctypes.c_int32 * max(2 * cap, 2))()
@@ -359,14 +359,23 @@ class VarlenLaunch:
             self.entries_ptr = None
         self.device = device
 
-    def _gathered(self, q: torch.Tensor, num_kv_heads: int) -> None:
-        """Gather mode: copy every entry's paged keys into the contiguous
-        buffer (allocated, and the contiguous entries uploaded, on the first
-        run of a shape), on the current stream."""
+    def _gathered(self, q: torch.Tensor, num_kv_heads: int) -> int:
+        """Gather mode: copy every entry's paged keys into a contiguous K/V
+        buffer on the current stream; returns the device address of the
+        entries over that buffer.
+
+        The buffer (and its uploaded entries) is allocated on the first run
+        of a (shape, stream) pair and reused by later runs on that stream,
+        which the stream orders after each other; a run on another stream
+        gets buffers of its own, so runs in flight on two streams never
+        overwrite each other's keys.  Each buffer holds ``total * Hkv * D``
+        16-bit elements of K and of V for as long as the launch lives."""
         g = self._gather
         head_dim = q.shape[2]
-        shape = (num_kv_heads, head_dim, q.dtype)
-        if g["shape"] != shape:
+        st = torch.cuda.current_stream(q.device)
+        key = (num_kv_heads, head_dim, q.dtype, st.cuda_stream)
+        buf = g["bufs"].get(key)
+        if buf is None:
             k = torch.empty(max(g["total"], 1), num_kv_heads, head_dim, dtype=q.dtype,
                             device=q.device)
             v = torch.empty_like(k)
@@ -375,14 +384,16 @@ class VarlenLaunch:
             cont["v_addr"] = v.data_ptr()
             cont["stride_tok"] = num_kv_heads * head_dim
             cont["stride_head"] = head_dim
-            g["k"], g["v"], g["shape"] = k, v, shape
-            g["cont_dev"], (self.entries_ptr,) = _upload([cont], q.device)
+            cont_dev, (ptr,) = _upload([cont], q.device)
+            buf = g["bufs"][key] = (k, v, cont_dev, ptr)
+        k, v, _cont_dev, ptr = buf
         L = _lib.lib()
         rc = L.hcp_gather_paged_kv(g["paged_ptr"], self.num_entries, g["start_ptr"],
                                    g["max_len"], num_kv_heads, head_dim,
-                                   _lib.dtype_code(q.dtype), g["k"].data_ptr(),
-                                   g["v"].data_ptr(), _lib.stream_ptr(q.device))
+                                   _lib.dtype_code(q.dtype), k.data_ptr(),
+                                   v.data_ptr(), _lib.stream_ptr(q.device))
         _lib.check(rc, "hcp_gather_paged_kv")
+        return ptr
 
     def run(self, q: torch.Tensor, out: torch.Tensor, lse: torch.Tensor | None,
             num_kv_heads: int, scale: float, window: int | None = None,
@@ -403,14 +414,15 @@ class VarlenLaunch:
         L = _lib.lib()
         win = int(window or 0) if self.causal else 0
         with torch.cuda.device(q.device):
+            entries_ptr = self.entries_ptr
             if self._gather is not None:
-                self._gathered(q, num_kv_heads)
+                entries_ptr = self._gathered(q, num_kv_heads)
             if acc is None:
                 rc = L.hcp_attn_fwd_varlen(
                     q.data_ptr(), q.stride(0), q.stride(1),
                     out.data_ptr(), out.stride(0), out.stride(1),
                     lse.data_ptr(), lse.stride(0),
-                    self.entries_ptr, self.num_entries,
+                    entries_ptr, self.num_entries,
                     self.tiles_ptr, self.num_tiles,
                     num_heads, num_kv_heads, head_dim, float(scale),
                     int(self.causal), win, int(self.paged),
@@ -425,7 +437,7 @@ class VarlenLaunch:
                 q.data_ptr(), q.stride(0), q.stride(1),
                 out.data_ptr(), out.stride(0), out.stride(1),
                 0 if lse is None else lse.data_ptr(), 0 if lse is None else lse.stride(0),
-                self.entries_ptr, self.num_entries,
+                entries_ptr, self.num_entries,
                 self.tiles_ptr, self.num_tiles,
                 num_heads, num_kv_heads, head_dim, float(scale),
                 int(self.causal), win, int(self.paged),

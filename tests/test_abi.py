@@ -242,6 +242,16 @@ def test_argument_validation_status_codes(L):
     assert _fwd(L, tq=0) == _lib.HCP_OK              # nothing to do, nothing launched
     assert _fwd(L, window=-1) == _lib.HCP_EINVAL
     assert b"negative window" in L.hcp_last_error()
+    # a K/V token stride the kernel's 32-bit tile offsets cannot step over
+    # (2^24 elements or more) is refused, as the varlen planner refuses it
+    big = 1 << 24
+    rc = L.hcp_attn_fwd_lse(16, 16, 16, 16, 16, 4, 4, 28, 4, 128, 8 * 28, 8, big, 8, big, 8,
+                            8 * 28, 8, 4, 0.088, 1, 0, 0, _lib.DTYPE_BF16, None)
+    assert rc == _lib.HCP_EUNSUPPORTED and b"2^24" in L.hcp_last_error()
+    rc = L.hcp_attn_fwd_lse_merge(16, 16, 16, 16, None, 4, 4, 28, 4, 128, 8 * 28, 8, big, 8,
+                                  big, 8, 8 * 28, 8, 4, 0.088, 1, 0, 0, 16, 8 * 28, 8, 16, 4, 1,
+                                  _lib.DTYPE_BF16, None)
+    assert rc == _lib.HCP_EUNSUPPORTED
     rc = L.hcp_merge_attn_states(16, 8, 8, 7, None, 0, 16, 8, 8, 1, 16, 4, 16, 8, 8, 1, 16, 4,
                                  4, 1, 8, None)
     assert rc == _lib.HCP_EUNSUPPORTED  # out dtype 7
@@ -398,3 +408,8 @@ def test_gather_paged_kv_status_codes(L):
     assert g(16, 3, 16, 10, 4, 128, _lib.DTYPE_BF16, 8, 16, 0) == _lib.HCP_EINVAL  # align
     assert g(16, 70000, 16, 10, 4, 128, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EINVAL
     assert "hcp_gather_paged_kv" in L.hcp_last_error().decode()
+    # a launch of max_len * heads * head_dim / 8 threads beyond 32 bits is
+    # refused on the host (grid.x * 256 must fit 32 bits): 2^28 rows at
+    # head_dim 128 is 2^32 threads
+    assert g(16, 3, 16, 1 << 26, 4, 128, _lib.DTYPE_BF16, 16, 16, 0) == _lib.HCP_EINVAL
+    assert "2^32" in L.hcp_last_error().decode()

@@ -253,3 +253,33 @@ def test_forward_decode_staged_plan_across_layers(dev, window):
         assert max_err(out, ref) <= OUT_TOL[torch.bfloat16], li
     assert rb.IMPL_STATS["decode_hip"] == 3
     assert sum(1 for k in rb._STEP["fast"] if k[0] == "dec_staged") == 1
+
+
+def test_forward_decode_staged_chunk_arriving_between_layers(dev):
+    """One decode request with no request-map entry takes the staged chunks
+    through the single-request fallback (ring_backend.py:738-748).  Layer 0
+    runs with nothing staged; a chunk is staged before layer 1, which must
+    attend to it -- the step's cached decode template is rebuilt when a chunk
+    key appears, not reused from layer 0."""
+    gen = torch.Generator().manual_seed(92)
+    peer, tk = 512, 512 + 300
+    seq_lens, qsl = [tk], [0, 1]
+    nb = -(-tk // BS) + 4
+    bt = _block_table(gen, seq_lens, nb)
+    meta = _meta(dev, qsl, seq_lens, bt)
+    impl = rb.HcpRingAttentionImpl(H, D, scale_for(D), HKV)
+    for li in range(3):
+        layer = types.SimpleNamespace(layer_name=f"model.layers.{li}.self_attn.attn")
+        cache = _cache(gen, "v031", nb, torch.bfloat16)
+        query = randn(gen, (1, H, D), torch.bfloat16)
+        peers = [None]
+        if li >= 1:
+            k, v = randn(gen, (peer, HKV, D), torch.bfloat16), randn(gen, (peer, HKV, D), torch.bfloat16)
+            rb.stage_peer_kv("late", layer.layer_name, k.to(dev), v.to(dev))
+            peers = [(k.float(), v.float())]
+        out = torch.empty(1, H, D, dtype=torch.bfloat16, device=dev)
+        impl.forward(layer, query.to(dev), None, None, cache.to(dev), meta, out)
+        torch.cuda.synchronize()
+        ref = orc.ring_forward(query.float(), cache.float(), "v031", qsl, seq_lens, bt,
+                               scale_for(D), peers=peers, out_dtype=torch.float32)
+        assert max_err(out, ref) <= OUT_TOL[torch.bfloat16], li

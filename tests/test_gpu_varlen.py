@@ -242,3 +242,41 @@ def test_gather_paged_kv_bit_exact(dev, bs):
             s = int(starts[r])
             assert torch.equal(k[s:s + L].cpu(), kr.to(dtype)), (layout, r)
             assert torch.equal(v[s:s + L].cpu(), vr.to(dtype)), (layout, r)
+
+
+def test_varlen_small_blocks_two_streams(dev):
+    """A gather-mode launch (block size 8) run on the current stream and on a
+    side stream: each stream gets its own contiguous K/V buffer, so runs in
+    flight on the two never share one; both results equal the oracle's."""
+    from hcp_vllm_plugin_amd.varlen import VarlenLaunch
+
+    h, hkv, d, dtype, bs = 14, 2, 128, torch.bfloat16, 8
+    lens, peers = [200, 64], [9, 0]
+    cache, bt, q, _ = _build(dev, "v031", lens, peers, h, hkv, d, dtype, bs, seed=77)
+    cd, btd, qd = cache.to(dev), bt.to(dev), q.to(dev)
+    pc = PagedCache.from_tensor(cd)
+    ent, qs = [], 0
+    for r, (L, P) in enumerate(zip(lens, peers)):
+        ent.append(make_entry(qs, L, segment_paged(pc, btd[r], P, L), 0))
+        qs += L
+    launch = VarlenLaunch(ent, True, True, dev)
+    scale = scale_for(d)
+    outs = []
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    for st in (torch.cuda.current_stream(dev), side):
+        with torch.cuda.stream(st):
+            o_ = torch.zeros_like(qd)
+            lse_ = torch.full((h, qd.shape[0]), float("-inf"), device=dev)
+            launch.run(qd, o_, lse_, hkv, scale)
+            outs.append((o_, lse_))
+    torch.cuda.synchronize()
+    assert len(launch._gather["bufs"]) == 2
+    for o_, lse_ in outs:
+        qs = 0
+        for r, (L, P) in enumerate(zip(lens, peers)):
+            kl, vl = orc.gather_paged(cache.float(), bt[r], P, L, "v031")
+            ro, rl = orc.attn_with_lse(q[qs:qs + L].float(), kl, vl, scale, 0)
+            assert max_err(o_[qs:qs + L], ro) <= OUT_TOL[dtype], r
+            assert max_err(lse_[:, qs:qs + L], rl) <= LSE_TOL, r
+            qs += L
