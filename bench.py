@@ -769,6 +769,95 @@ def cpu_baseline(budget_s=30.0):
     }
 
 
+def cpu_baseline_configs(threads: int) -> dict:
+    """The CPU oracle on bounded samples of the other workloads, each in the
+    unit of its GPU line: the batch-64 split-KV decode (four sequences of its
+    shape: 32768 peer + U[512, 2048] local keys, GB/s of K/V read), the
+    16-request varlen batch (two requests of its length distribution,
+    TFLOP/s) and the Llama-3-70B 128k layer (1024 queries of chunk 0 for one
+    KV-head group; the whole layer's CPU time is extrapolated from that rate
+    and stated as such).  Seeded CPU inputs of the same shapes: the rate does
+    not depend on the values."""
+    from oracle import ring_oracle as orc
+
+    host = cpu_host_info()
+    common = {"cores": threads, "threads": threads, "cpu_model": host["cpu_model"],
+              "kind": "port"}
+
+    def ring_rows(q, kl, vl, kp, vp, off):
+        """local causal at `off` over kl/vl, peer over kp/vp, merged (oracle)"""
+        o_l, l_l = orc.attn_with_lse(q, kl, vl, SCALE, off)
+        o_p, l_p = orc.attn_with_lse(q, kp, vp, SCALE, None)
+        return orc.merge_pair(o_p, l_p, o_l, l_l)
+
+    gen = torch.Generator().manual_seed(11)
+    res = {}
+    # decode: one query per sequence over its peer chunk and local keys
+    seqs, peer_len = 4, 32768
+    loc = torch.randint(512, 2049, (seqs,), generator=gen).tolist()
+    t_dec, nbytes = 0.0, 0
+    for s in range(seqs):
+        q = torch.randn(1, H, D, generator=gen).to(torch.bfloat16).float()
+        kp, vp = (torch.randn(peer_len, HKV, D, generator=gen).to(torch.bfloat16).float()
+                  for _ in range(2))
+        kl, vl = (torch.randn(loc[s], HKV, D, generator=gen).to(torch.bfloat16).float()
+                  for _ in range(2))
+        t0 = time.perf_counter()  # the oracle's own time, not the input draws
+        ring_rows(q, kl, vl, kp, vp, loc[s] - 1)
+        t_dec += time.perf_counter() - t0
+        nbytes += (peer_len + loc[s]) * HKV * D * 2 * 2 + H * D * 2 * 2
+    res["decode"] = {**common, "value": round(nbytes / t_dec / 1e9, 2), "unit": "GB/s",
+                     "ms_per_sequence": round(t_dec * 1e3 / seqs, 1),
+                     "sample": (f"{seqs} decode sequences of the batch-64 shape (32768 peer + "
+                                f"U[512,2048] local keys, 28/4 heads): local causal + peer + "
+                                f"merge per sequence, {nbytes / 1e9:.3f} GB of K/V in "
+                                f"{t_dec:.2f} s, {threads} threads")}
+    # varlen: two requests, local causal over their own keys + peer prefix
+    loc = torch.randint(512, 4097, (2,), generator=gen).tolist()
+    pre = (16 * torch.randint(64, 1025, (2,), generator=gen)).tolist()
+    flops, t_var = 0, 0.0
+    for r in range(2):
+        q = torch.randn(loc[r], H, D, generator=gen).to(torch.bfloat16).float()
+        kl, vl = (torch.randn(loc[r], HKV, D, generator=gen).to(torch.bfloat16).float()
+                  for _ in range(2))
+        kp, vp = (torch.randn(pre[r], HKV, D, generator=gen).to(torch.bfloat16).float()
+                  for _ in range(2))
+        g = H // HKV
+        t0 = time.perf_counter()
+        for j in range(HKV):  # one KV-head group at a time bounds the score buffers
+            sl, hs = slice(j, j + 1), slice(j * g, (j + 1) * g)
+            ring_rows(q[:, hs], kl[:, sl], vl[:, sl], kp[:, sl], vp[:, sl], 0)
+        t_var += time.perf_counter() - t0
+        flops += 4 * D * H * (causal_pairs(loc[r], loc[r], 0) + loc[r] * pre[r])
+    res["varlen16_paged"] = {**common, "value": round(flops / t_var / 1e12, 4),
+                             "unit": "TFLOP/s",
+                             "sample": (f"2 requests of the varlen batch's distribution "
+                                        f"(local {loc} causal + peer {pre}, 28/4 heads), one "
+                                        f"KV-head group at a time: {flops / 1e12:.3f} TFLOP in "
+                                        f"{t_var:.2f} s, {threads} threads")}
+    # Llama-3-70B layer: 1024 queries of chunk 0, one KV-head group (8 heads)
+    h70, hkv70, rows, n = 64, 8, 1024, 65536
+    g = h70 // hkv70
+    q = torch.randn(rows, g, D, generator=gen).to(torch.bfloat16).float()
+    kl, vl = (torch.randn(rows, 1, D, generator=gen).to(torch.bfloat16).float() for _ in range(2))
+    kp, vp = (torch.randn(n, 1, D, generator=gen).to(torch.bfloat16).float() for _ in range(2))
+    t0 = time.perf_counter()
+    ring_rows(q, kl, vl, kp, vp, 0)
+    t70 = time.perf_counter() - t0
+    f_sample = 4 * D * g * (causal_pairs(rows, rows, 0) + rows * n)
+    pairs_layer = sum(causal_pairs(8192, 8192 * (c + 1), 8192 * c) for c in range(8)) + n * n
+    f_layer = 4 * D * h70 * pairs_layer
+    rate = f_sample / t70
+    res["llama70b_128k"] = {**common, "value": round(rate / 1e12, 4), "unit": "TFLOP/s",
+                            "layer_s_extrapolated": round(f_layer / rate, 1),
+                            "sample": (f"{rows} queries of chunk 0 (local causal over its {rows} "
+                                       f"keys + 65536 peer keys + merge) for one KV-head group "
+                                       f"(8 of 64 heads): {f_sample / 1e12:.3f} TFLOP in "
+                                       f"{t70:.2f} s, {threads} threads; the whole layer "
+                                       f"({f_layer / 1e12:.1f} TFLOP) extrapolated at that rate")}
+    return res
+
+
 def cpu_host_info() -> dict:
     """The host CPU as the CPU baseline uses it.
 
@@ -821,6 +910,11 @@ def copy_probe(dev, mib=1024, reps=3):
         y.copy_(x)
     torch.cuda.synchronize()
     return {"copy_mib": mib, "reps": reps}
+
+
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes "
+                  "over this bench's workload (committed, not measured in this run), scaled "
+                  "by a 1 GiB device copy's counts")
 
 
 def load_traffic():
@@ -912,6 +1006,8 @@ def main():
         extra["decode_forward_staged"] = bench_decode_forward(dev, args.steps, args.warmup)
         extra["head_dim_256"] = bench_head_dim_256(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
+    cpu_cfg = (None if args.no_cpu_baseline or (args.no_decode and args.no_configs)
+               else cpu_baseline_configs(cpu["threads"]))
     traffic = load_traffic()
 
     value = pre["flops"] / (pre["ms_per_step"] * 1e-3) / 1e12
@@ -946,6 +1042,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(peer_tf / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic.get("fa_fwd_peer", {}).get("bytes"),
+            "traffic_source": TRAFFIC_SOURCE if traffic else None,
         },
         "kernels": {
             "local_causal_merged": {"ms": round(pre["local"]["ms"], 4),
@@ -983,9 +1080,15 @@ def main():
                 "unit": "GB/s",
                 "frac": round(dec["gbs"] / PEAK_HBM_GBS, 4),
                 "traffic": traffic.get("decode_split", {}).get("bytes"),
+                "traffic_source": TRAFFIC_SOURCE if traffic else None,
             },
         }
+        if cpu_cfg:
+            line["decode"]["cpu_baseline"] = cpu_cfg["decode"]
     if extra:
+        if cpu_cfg:
+            for k in ("varlen16_paged", "llama70b_128k"):
+                extra[k]["cpu_baseline"] = cpu_cfg[k]
         line["configs"] = extra
     print(json.dumps(line), flush=True)
 

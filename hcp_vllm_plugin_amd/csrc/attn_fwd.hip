@@ -447,6 +447,9 @@ fa_fwd_kernel(FwdParams p) {
   // (-inf until the row has seen a key).  O and l are relative to it.
   const float c = p.scale_log2;
   float m_ref = -INFINITY;
+  // -m_ref for the exponent's FMA (0 while the row has seen no key), kept
+  // with m_ref rather than formed again on every tile
+  float m_neg = 0.f;
   float l_run = 0.f;   // sum of P in f32: the LSE
   float lr_run = 0.f;  // sum of P as rounded for the PV product: normalises O
   f32x16 oacc[DBLK];
@@ -558,6 +561,7 @@ fa_fwd_kernel(FwdParams p) {
     for (int i = 0; i < DBLK; ++i) oacc[i] *= alpha;
     acc_fence();
     m_ref = m_new;
+    m_neg = m_new == -INFINITY ? 0.f : -m_new;
   };
 
   // One iteration n of the software pipeline, S_cur = scores of tile n
@@ -594,29 +598,34 @@ fa_fwd_kernel(FwdParams p) {
   // P for score pair `pair` (scores 2*pair, 2*pair+1 of the lane's 32):
   // exp2(c S - m) packed into its P^T fragment (S is kept) and added to the
   // lane's tile sums (two chains)
-  auto exp_pair = [&](int pair, const f32x16 (&Sc)[2], float m_use, float (&ts)[4])
+  auto exp_pair = [&](int pair, const f32x16 (&Sc)[2], float (&ts)[4])
       __attribute__((always_inline)) {
     const int x = 2 * pair;  // 0..31, even
     const int h = x >> 4, r = x & 15;
-    const float p0 = fast_exp2(__builtin_fmaf(Sc[h][r], c, -m_use));
-    const float p1 = fast_exp2(__builtin_fmaf(Sc[h][r + 1], c, -m_use));
+    const float p0 = fast_exp2(__builtin_fmaf(Sc[h][r], c, m_neg));
+    const float p1 = fast_exp2(__builtin_fmaf(Sc[h][r + 1], c, m_neg));
     // P^T fragment 2h + (r >> 3) holds regs 8t .. 8t+7 of half h
     u32x4 w = __builtin_bit_cast(u32x4, pf[2 * h + (r >> 3)]);
     const uint32_t pw = pack2<T>(p0, p1);
     w[(r & 7) >> 1] = pw;
     pf[2 * h + (r >> 3)] = as_vec8<V8>(w);
-    ts[0] += p0;
-    ts[1] += p1;
-    ts[2 + (pair & 1)] = sum2<T>(pw, ts[2 + (pair & 1)]);
+    // the tile's sums start at its first pairs (P >= 0: no signed zero to
+    // keep, and no accumulator to clear)
+    if (pair == 0) {
+      ts[0] = p0;
+      ts[1] = p1;
+    } else {
+      ts[0] += p0;
+      ts[1] += p1;
+    }
+    ts[2 + (pair & 1)] = pair < 2 ? sum2_first<T>(pw) : sum2<T>(pw, ts[2 + (pair & 1)]);
   };
   // the rare path of a tile whose P would exceed 2^12 (or a row with no
   // reference yet): rescale to the tile's true row max, form P again
   auto redo_tile = [&](const f32x16 (&Sc)[2], float (&ts)[4]) __attribute__((always_inline)) {
     rescale_to(tile_max(Sc));
-    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-    ts[0] = ts[1] = ts[2] = ts[3] = 0.f;
 #pragma unroll
-    for (int pr = 0; pr < 16; ++pr) exp_pair(pr, Sc, m_use, ts);
+    for (int pr = 0; pr < 16; ++pr) exp_pair(pr, Sc, ts);
   };
   constexpr int NA = 2 * KSTEPS;  // MFMAs in phase A
   constexpr int EA = 32 / NA;     // scores exponentiated per phase-A MFMA
@@ -629,7 +638,6 @@ fa_fwd_kernel(FwdParams p) {
     // issue ahead of the other wave on the SIMD, whose MFMAs (often its phase
     // B) keep the matrix pipe busy meanwhile.  Phase B drops it again.
     __builtin_amdgcn_s_setprio(1);
-    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     constexpr int KR = HCP_KPF + 1;  // K fragment ring
     V8 kf[KR];
 #pragma unroll
@@ -658,9 +666,9 @@ fa_fwd_kernel(FwdParams p) {
       // every second MFMA)
       if constexpr (EA >= 2) {
 #pragma unroll
-        for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, m_use, ts);
+        for (int q = 0; q < EA; q += 2) exp_pair((st * EA + q) >> 1, Sc, ts);
       } else if (st & 1) {
-        exp_pair(st >> 1, Sc, m_use, ts);
+        exp_pair(st >> 1, Sc, ts);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -720,7 +728,7 @@ fa_fwd_kernel(FwdParams p) {
       rsv = tile_rsrc(vseg, n + 1);
     }
     if (n < wtiles) {
-      float ts[4] = {0.f, 0.f, 0.f, 0.f};
+      float ts[4];  // the tile's P sums (phase A sets all four)
       phase_a(Ks, Sc, Sn, rsk, kload, rsv, vload, ts);
       if (__any(ts[0] + ts[1] > kSumThresh || m_ref == -INFINITY)) redo_tile(Sc, ts);
       l_run += ts[0] + ts[1];

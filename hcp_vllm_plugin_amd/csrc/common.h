@@ -104,6 +104,24 @@ __device__ __forceinline__ float sum2<_Float16>(uint32_t w, float acc) {
                                 __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
 }
 
+// lo + hi of a dword of two 16-bit elements, in f32 (sum2 with a zero
+// accumulator, as the three-operand v_dot2 with an inline 0: no register
+// to clear first)
+template <typename T>
+__device__ __forceinline__ float sum2_first(uint32_t w);
+template <>
+__device__ __forceinline__ float sum2_first<__bf16>(uint32_t w) {
+  float r;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(w), "v"(0x3f803f80u));
+  return r;
+}
+template <>
+__device__ __forceinline__ float sum2_first<_Float16>(uint32_t w) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(w), "v"(0x3c003c00u));
+  return r;
+}
+
 template <typename V>
 __device__ __forceinline__ V as_vec8(u32x4 x) {
   return __builtin_bit_cast(V, x);

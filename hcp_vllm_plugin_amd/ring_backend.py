@@ -308,13 +308,44 @@ def _contiguous_record(j: int, seq: int, k: torch.Tensor, v: torch.Tensor):
 # metadata object, so one device->host copy serves all layers of a step (the
 # reference syncs three times per layer, ring_backend.py:604-605).  Holding the
 # object keeps its identity from being reused by a later step's metadata.
-_STEP: dict = {"meta": None, "host": None, "bt": None, "fast": {}}
+_STEP: dict = {"meta": None, "stamp": None, "host": None, "bt": None, "fast": {}}
+
+
+def _version_of(t: torch.Tensor) -> int:
+    try:
+        return t._version
+    except RuntimeError:  # inference-mode tensors keep no version counter
+        return -1
+
+
+def _meta_stamp(attn_metadata) -> tuple:
+    """What identifies one step's metadata contents without reading them:
+    the object, and the storage, shape and in-place version counter of each
+    tensor the forward reads.  A caller that keeps one metadata object and
+    refills its tensors in place between steps through torch's in-place ops
+    bumps the version counters, so the next step does not reuse the previous
+    step's host copy or plans.  (vLLM builds a new metadata object every
+    step; tensors made under inference mode keep no version counter, and a
+    caller that refills such tensors in one reused object calls
+    ``invalidate_step_cache`` between steps.)"""
+    st = [id(attn_metadata)]
+    for t in (attn_metadata.query_start_loc, attn_metadata.seq_lens, attn_metadata.block_table):
+        st.extend((t.data_ptr(), tuple(t.shape), _version_of(t)))
+    return tuple(st)
+
+
+def invalidate_step_cache() -> None:
+    """Drop the cached host copy of the step's metadata and the plans built
+    from it: for a caller that rewrites the metadata tensors behind torch's
+    back (a kernel writing into them directly) before reusing the object."""
+    _STEP.update(meta=None, stamp=None, host=None, bt=None, fast={})
 
 
 def _host_metadata(attn_metadata):
     """(query_start_loc, seq_lens, first block ids) as lists, and the block
     table as contiguous int32, for this step's metadata."""
-    if _STEP["meta"] is attn_metadata:
+    stamp = _meta_stamp(attn_metadata)
+    if _STEP["meta"] is attn_metadata and _STEP.get("stamp") == stamp:
         return _STEP["host"], _STEP["bt"]
     block_table = attn_metadata.block_table
     if block_table.dtype != torch.int32:
@@ -327,7 +358,7 @@ def _host_metadata(attn_metadata):
     packed = torch.cat([qsl_t.reshape(-1).to(torch.int64), sl_t.reshape(-1).to(torch.int64),
                         fb.reshape(-1).to(torch.int64)]).tolist()
     host = (packed[:n + 1], packed[n + 1:2 * n + 1], packed[2 * n + 1:])
-    _STEP.update(meta=attn_metadata, host=host, bt=block_table, fast={})
+    _STEP.update(meta=attn_metadata, stamp=stamp, host=host, bt=block_table, fast={})
     return host, block_table
 
 

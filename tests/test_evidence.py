@@ -94,3 +94,32 @@ def test_staging_generation_moves_only_on_key_or_map_changes():
     rb.stage_peer_kv("a", "l0", k, k)   # the key appears again
     assert rb._STAGE_GEN[0] > g4
     rb.clear_peer_kv()
+
+
+def test_step_metadata_cache_sees_in_place_updates():
+    """The host copy of a step's metadata is reused while the same object and
+    the same tensor contents (by storage, shape and in-place version) come
+    back, and rebuilt when a reused object's tensors are refilled in place
+    between steps, or after invalidate_step_cache()."""
+    import types
+
+    bt = torch.tensor([[3, 4], [5, 6]], dtype=torch.int32)
+    meta = types.SimpleNamespace(query_start_loc=torch.tensor([0, 2, 5], dtype=torch.int32),
+                                 seq_lens=torch.tensor([10, 20], dtype=torch.int32),
+                                 block_table=bt)
+    (qsl, sl, fb), _ = rb._host_metadata(meta)
+    assert (qsl, sl, fb) == ([0, 2, 5], [10, 20], [3, 5])
+    rb._STEP["fast"]["x"] = 1
+    assert rb._host_metadata(meta)[0][1] == [10, 20] and "x" in rb._STEP["fast"]
+    meta.seq_lens.copy_(torch.tensor([11, 21]))  # refilled in place: next step
+    (qsl, sl, fb), _ = rb._host_metadata(meta)
+    assert sl == [11, 21] and "x" not in rb._STEP["fast"]
+    meta.block_table[1, 0] = 9
+    assert rb._host_metadata(meta)[0][2] == [3, 9]
+    with torch.inference_mode():
+        qi = torch.tensor([0, 1, 2], dtype=torch.int32)
+    meta.query_start_loc = qi  # no version counter: explicit invalidation
+    assert rb._host_metadata(meta)[0][0] == [0, 1, 2]
+    rb._STEP["fast"]["y"] = 1
+    rb.invalidate_step_cache()
+    assert rb._host_metadata(meta)[0][0] == [0, 1, 2] and "y" not in rb._STEP["fast"]
