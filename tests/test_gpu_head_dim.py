@@ -201,9 +201,11 @@ def test_rescale_path_d256(dev, dtype, off, slope, spike):
 
 def test_ring_step_d256_full_size(dev):
     """The head_dim 256 bench shape (16 / 8 heads, bf16): the 8192-key peer
-    pass, then the 8192-key local causal pass merging it; sampled rows against
-    the oracle, and the whole output against one causal pass over [peer; local]
-    (the ring step's identity)."""
+    pass, then the 8192-key local causal pass merging it; every row of out and
+    LSE against the oracle's ring step, and the whole output against one
+    causal pass over [peer; local] (the ring step's identity)."""
+    from tests.test_gpu_fullsize import _oracle_ring
+
     h, hkv, d, n = 16, 8, 256, 8192
     g = torch.Generator(device=dev).manual_seed(256)
     ch = torch.randperm(d, generator=torch.Generator().manual_seed(3))[:4]
@@ -226,8 +228,6 @@ def test_ring_step_d256_full_size(dev):
     assert torch.isfinite(out).all() and torch.isfinite(lse).all()
     assert max_err(out, o1) <= 2 * OUT_TOL[torch.bfloat16]
     assert max_err(lse, l1) <= 2 * LSE_TOL
-    kc, vc = kk.float().cpu(), vv.float().cpu()
-    for r0 in (0, 3000, 8176):
-        ro, rl = orc.attn_with_lse(q[r0:r0 + 16].float().cpu(), kc, vc, scale, n + r0)
-        assert max_err(out[r0:r0 + 16], ro) <= OUT_TOL[torch.bfloat16], r0
-        assert max_err(lse[:, r0:r0 + 16], rl) <= LSE_TOL, r0
+    ro, rl = _oracle_ring(q, kl, vl, kp, vp, scale, 0, hkv)
+    assert max_err(out, ro) <= OUT_TOL[torch.bfloat16], max_err(out, ro)
+    assert max_err(lse, rl) <= LSE_TOL, max_err(lse, rl)
