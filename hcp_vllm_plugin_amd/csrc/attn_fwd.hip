@@ -400,12 +400,14 @@ fa_fwd_kernel(FwdParams p) {
   // and four V offsets per half cover any D (D = 256 rows have 32 slots).
   // K (A operand of S^T): row 32*blk + r32, 16-byte chunk 2s+g
   // (row + 32 has the same swizzle, so block 1 is an immediate offset)
-  // D = 256 (one wave per SIMD, every register in use): each offset is the
-  // first one XOR a constant, formed where it is used -- the row's slot
-  // bits (4..8) are disjoint from the row's own offset, so offset(s) =
-  // offset(0) ^ 32 s for K and offset(db) = offset(0) ^ 64 db for V -- by an
-  // opaque XOR the compiler cannot hoist into a loop-long register.
-  constexpr bool kXorOfs = D == 256;
+  // D = 256 non-causal (one wave per SIMD, every register in use): each
+  // offset is the first one XOR a constant, formed where it is used -- the
+  // row's slot bits (4..8) are disjoint from the row's own offset, so
+  // offset(s) = offset(0) ^ 32 s for K and offset(db) = offset(0) ^ 64 db for
+  // V -- by an opaque XOR the compiler cannot hoist into a loop-long register.
+  // The causal kernels keep the offsets in registers (they fit without
+  // spilling there, and the extra XOR per LDS read costs 3% of the step).
+  constexpr bool kXorOfs = D == 256 && !CAUSAL;
   auto xor_ofs = [&](int base, int c) __attribute__((always_inline)) {
     if (c == 0) return base;
     int r;
