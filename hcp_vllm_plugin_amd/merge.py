@@ -41,7 +41,21 @@ def merge_attn_states(
     suffix_lse: torch.Tensor,
     output_lse: torch.Tensor | None = None,
 ) -> None:
-    """out = (e^{lse_p} o_p + e^{lse_s} o_s) / (e^{lse_p} + e^{lse_s}); in place."""
+    """out = (e^{lse_p} o_p + e^{lse_s} o_s) / (e^{lse_p} + e^{lse_s}); in place.
+
+    A head_dim that is not a multiple of 8 runs on zero-padded copies (the
+    kernel moves 16-byte pieces), the result copied back into ``output``."""
+    if output.dim() == 3 and output.shape[2] % 8:
+        from .ring_attn import pad_head_dim, padded_width
+
+        if prefix_output.shape != output.shape or suffix_output.shape != output.shape:
+            raise ValueError("output / prefix_output / suffix_output shapes differ")
+        w = padded_width(output.shape[2])
+        tmp = output.new_empty((output.shape[0], output.shape[1], w))
+        merge_attn_states(tmp, pad_head_dim(prefix_output, w), prefix_lse,
+                          pad_head_dim(suffix_output, w), suffix_lse, output_lse)
+        output.copy_(tmp[..., : output.shape[2]])
+        return
     for n, t in (("output", output), ("prefix_output", prefix_output),
                  ("suffix_output", suffix_output)):
         _chk_o(n, t)

@@ -17,7 +17,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["ring_attn_with_lse", "ring_attn_merged", "check_qkv", "COPY_STATS"]
+__all__ = ["ring_attn_with_lse", "ring_attn_merged", "check_qkv", "COPY_STATS",
+           "pad_head_dim", "padded_width"]
 
 # Layout copies made on the way into the kernels: an input whose layout the
 # kernel cannot load directly (rows not 16-byte aligned, strides not
@@ -52,6 +53,25 @@ def check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise ValueError("head_dim must be the contiguous dimension")
 
 
+def pad_head_dim(t: torch.Tensor, width: int) -> torch.Tensor:
+    """t ``[T, heads, d]`` copied into a zero-filled ``[T, heads, width]``
+    (counted in COPY_STATS).  The kernels load rows in 16-byte pieces, so a
+    head_dim that is not a multiple of 8 runs at the next multiple of 8: zero
+    columns in q and k add nothing to the scores, and zero columns of v give
+    output columns that are dropped -- the reference's masked ``BLOCK_D``
+    columns (ring_triton_attn.py:69-78,201)."""
+    out = t.new_zeros((t.shape[0], t.shape[1], width))
+    out[..., : t.shape[2]].copy_(t)
+    COPY_STATS["tensors"] += 1
+    COPY_STATS["bytes"] += out.numel() * out.element_size()
+    return out
+
+
+def padded_width(head_dim: int) -> int:
+    """The multiple of 8 a head_dim runs at."""
+    return -(-head_dim // 8) * 8
+
+
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     """Return t, or a contiguous copy when its layout is not kernel-loadable."""
     ok = (
@@ -83,6 +103,11 @@ def ring_attn_with_lse(
     check_qkv(q, k, v)
     if window is not None and window <= 0:
         raise ValueError("window must be a positive number of keys")
+    if q.shape[2] % 8:
+        w = padded_width(q.shape[2])
+        out, lse = ring_attn_with_lse(pad_head_dim(q, w), pad_head_dim(k, w), pad_head_dim(v, w),
+                                      scale, causal_offset, window)
+        return out[..., : q.shape[2]].contiguous(), lse
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     tq, num_heads, head_dim = q.shape
     tk, num_kv_heads = k.shape[0], k.shape[1]
@@ -147,6 +172,17 @@ def ring_attn_merged(
     check_qkv(q, k, v)
     if window is not None and window <= 0:
         raise ValueError("window must be a positive number of keys")
+    if q.shape[2] % 8:
+        if output is not None and (output.shape != q.shape or output.dtype != q.dtype):
+            raise ValueError("output must match q in shape and dtype")
+        w = padded_width(q.shape[2])
+        res = ring_attn_merged(pad_head_dim(q, w), pad_head_dim(k, w), pad_head_dim(v, w),
+                               scale, causal_offset, pad_head_dim(acc_output, w), acc_lse,
+                               acc_is_prefix, window, None, output_lse)
+        if output is None:
+            return res[..., : q.shape[2]].contiguous()
+        output.copy_(res[..., : q.shape[2]])
+        return output
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     _check_partial(acc_output, acc_lse, q, "acc")
     tq, num_heads, head_dim = q.shape

@@ -582,6 +582,11 @@ class HcpRingAttentionImpl(_ImplBase):  # type: ignore[misc,valid-type]
             raise ValueError("sliding_window must be a positive number of keys")
         if kv_cache_dtype not in ("auto", "float16", "bfloat16"):
             raise NotImplementedError(f"kv_cache_dtype {kv_cache_dtype} not supported")
+        # the paged cache is read in place in 16-byte pieces (vLLM's flash
+        # backends take the same head sizes)
+        if head_size % 8 or not 0 < head_size <= 256:
+            raise NotImplementedError(
+                f"HCP ring backend: head_size {head_size} not supported (a multiple of 8 up to 256)")
         # applied to every causal pass (local segments), never to the
         # non-causal peer pass -- ring_backend.py:490-492,786,815,826-830
         self.sliding_window = int(sliding_window) if sliding_window is not None else None

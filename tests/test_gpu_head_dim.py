@@ -51,6 +51,41 @@ def test_forward_head_dims(dev, d, dtype, off):
     assert max_err(lse, rl) <= LSE_TOL
 
 
+@pytest.mark.parametrize("d", [1, 3, 20, 100, 130, 250])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_kernel_contract_any_head_dim(dev, d, dtype):
+    """head_dims that are not a multiple of 8 (the reference's kernel takes any,
+    with masked BLOCK_D columns, ring_triton_attn.py:69-78,201): the pass
+    (causal and not), the merging pass and merge_attn_states / merge_pair run
+    on zero-padded copies and return [T, H, d] results equal to the oracle's."""
+    from hcp_vllm_plugin_amd import merge_pair
+
+    gen = torch.Generator().manual_seed(900 + d)
+    tq, tk, h, hkv = 150, 333, 6, 2
+    q = randn(gen, (tq, h, d), dtype)
+    k = randn(gen, (tk, hkv, d), dtype)
+    v = randn(gen, (tk, hkv, d), dtype)
+    kp, vp = randn(gen, (200, hkv, d), dtype), randn(gen, (200, hkv, d), dtype)
+    scale = scale_for(d)
+    qd, kd, vd, kpd, vpd = (t.to(dev) for t in (q, k, v, kp, vp))
+    o_l, l_l = ring_attn_with_lse(qd, kd, vd, scale, tk - tq)
+    o_p, l_p = ring_attn_with_lse(qd, kpd, vpd, scale, None)
+    out = torch.empty_like(o_l)
+    merge_attn_states(out, o_p, l_p, o_l, l_l)
+    mo, ml = merge_pair(o_p, l_p, o_l, l_l)
+    fused = ring_attn_merged(qd, kd, vd, scale, tk - tq, o_p, l_p)
+    torch.cuda.synchronize()
+    assert o_l.shape == (tq, h, d) and out.shape == (tq, h, d) and fused.shape == (tq, h, d)
+    rl, rll = orc.attn_with_lse(q.float(), k.float(), v.float(), scale, tk - tq)
+    rp, rpl = orc.attn_with_lse(q.float(), kp.float(), vp.float(), scale, None)
+    rm = orc.lse_merge(rl, rll, rp, rpl)
+    assert max_err(o_l, rl) <= OUT_TOL[dtype] and max_err(l_l, rll) <= LSE_TOL
+    assert max_err(o_p, rp) <= OUT_TOL[dtype] and max_err(l_p, rpl) <= LSE_TOL
+    assert max_err(out, rm) <= OUT_TOL[dtype]
+    assert torch.equal(mo, out) and torch.equal(fused, out)
+    assert max_err(ml, torch.logaddexp(rll, rpl)) <= LSE_TOL
+
+
 @pytest.mark.parametrize("d", [40, 96, 256])
 def test_merged_pass_head_dims(dev, d):
     """Local pass merging a peer partial (the acc epilogue) equals pass +
