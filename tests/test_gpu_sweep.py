@@ -1,6 +1,8 @@
-"""GPU parity sweep of HcpRingAttentionImpl.forward over seeded random
-configurations, against the oracle's restated segmentation
-(oracle.ring_oracle.ring_forward, ring_backend.py:576-834).
+"""GPU parity sweeps over seeded random configurations: of
+HcpRingAttentionImpl.forward against the oracle's restated segmentation
+(oracle.ring_oracle.ring_forward, ring_backend.py:576-834), and of the
+kernel contract (ring_attn_with_lse / ring_attn_merged) against the oracle's
+_attn_with_lse and merge (ring_backend.py:366-421, ring_decode.py:46-61).
 
 Each case draws, from its own seed: the head counts (any GQA group), a
 head_dim (a multiple of 8 up to 256), the dtype, the cache layout and block
@@ -133,3 +135,59 @@ def test_forward_random_configuration(dev, seed, monkeypatch):
     assert max_err(output[:n], ref[:n]) <= OUT_TOL[dtype], (c, max_err(output[:n], ref[:n]))
     assert torch.all(output[n:] == 7.0)
     assert rb.IMPL_STATS["attn_torch"] == 0 and rb.IMPL_STATS["merge_torch"] == 0
+
+
+def _draw_pass(seed):
+    """A kernel-contract case (plain Python values) drawn from ``seed``."""
+    rnd = random.Random(seed)
+    hkv = rnd.choice([1, 2, 4, 8])
+    group = rnd.choice([1, 2, 4, 7, 8])
+    d = rnd.choice([64, 128, rnd.randint(1, 256)])
+    tq = rnd.randint(1, 1200)
+    tk = rnd.randint(0, 2000)
+    causal = rnd.random() < 0.6
+    off = rnd.choice([tk - tq, rnd.randint(-200, tk + 200)]) if causal else None
+    window = rnd.choice([None, rnd.randint(1, 800)]) if causal else None
+    return dict(h=hkv * group, hkv=hkv, d=d, tq=tq, tk=tk, off=off, window=window,
+                dtype=rnd.choice([torch.bfloat16, torch.float16]),
+                packed=rnd.random() < 0.3, merged=rnd.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_pass_random_configuration(dev, seed):
+    """``ring_attn_with_lse`` (and, for half the cases, ``ring_attn_merged``
+    over a random partial) on random shapes: any head_dim up to 256, causal
+    offsets inside, before and past the key range, windows, empty key ranges,
+    and q/k/v as views into one packed projection output -- against the
+    oracle's ``_attn_with_lse`` / merge restatement."""
+    from hcp_vllm_plugin_amd import ring_attn_merged, ring_attn_with_lse
+    from tests._util import LSE_TOL
+
+    c = _draw_pass(5000 + seed)
+    h, hkv, d, tq, tk, dtype = c["h"], c["hkv"], c["d"], c["tq"], c["tk"], c["dtype"]
+    print(f"pass case {seed}: {c}", flush=True)
+    gen = torch.Generator().manual_seed(seed)
+    if c["packed"]:  # one projection output [T, H + 2 Hkv, D]; q, k, v are views
+        t = max(tq, tk)
+        qkv = randn(gen, (t, h + 2 * hkv, d), dtype).to(dev)
+        q, k, v = qkv[:tq, :h], qkv[:tk, h:h + hkv], qkv[:tk, h + hkv:]
+    else:
+        q = randn(gen, (tq, h, d), dtype).to(dev)
+        k = randn(gen, (tk, hkv, d), dtype).to(dev)
+        v = randn(gen, (tk, hkv, d), dtype).to(dev)
+    scale = scale_for(d)
+    ro, rl = orc.attn_with_lse(q.float().cpu(), k.float().cpu(), v.float().cpu(), scale,
+                               c["off"], window=c["window"])
+    if c["merged"]:
+        po = randn(gen, (tq, h, d), dtype).to(dev)
+        pl = (torch.randn(h, tq, generator=gen) * 3).to(dev)
+        lse = torch.empty(h, tq, dtype=torch.float32, device=dev)
+        out = ring_attn_merged(q, k, v, scale, c["off"], po, pl, window=c["window"],
+                               output_lse=lse)
+        ro, rl = orc.merge_pair(po.float().cpu(), pl.cpu(), ro, rl)
+    else:
+        out, lse = ring_attn_with_lse(q, k, v, scale, c["off"], window=c["window"])
+    torch.cuda.synchronize()
+    assert out.shape == (tq, h, d) and out.dtype == dtype
+    assert max_err(out, ro) <= OUT_TOL[dtype], (c, max_err(out, ro))
+    assert max_err(lse, rl) <= LSE_TOL, (c, max_err(lse, rl))
