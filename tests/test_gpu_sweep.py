@@ -167,19 +167,26 @@ def test_pass_random_configuration(dev, seed):
     h, hkv, d, tq, tk, dtype = c["h"], c["hkv"], c["d"], c["tq"], c["tk"], c["dtype"]
     print(f"pass case {seed}: {c}", flush=True)
     gen = torch.Generator().manual_seed(seed)
+    # values at half scale: with a handful of keys a row's output is close to
+    # one value row, and an N(0,1) row reaches |o| > 4, where bf16's own
+    # rounding (half an ulp, 2^-6) is above the 1.5e-2 gate for any
+    # implementation
     if c["packed"]:  # one projection output [T, H + 2 Hkv, D]; q, k, v are views
         t = max(tq, tk)
-        qkv = randn(gen, (t, h + 2 * hkv, d), dtype).to(dev)
+        qkv = randn(gen, (t, h + 2 * hkv, d), torch.float32)
+        qkv[:, h + hkv:] *= 0.5
+        qkv = qkv.to(dtype).to(dev)
         q, k, v = qkv[:tq, :h], qkv[:tk, h:h + hkv], qkv[:tk, h + hkv:]
     else:
         q = randn(gen, (tq, h, d), dtype).to(dev)
         k = randn(gen, (tk, hkv, d), dtype).to(dev)
-        v = randn(gen, (tk, hkv, d), dtype).to(dev)
+        v = (randn(gen, (tk, hkv, d), torch.float32) * 0.5).to(dtype).to(dev)
     scale = scale_for(d)
     ro, rl = orc.attn_with_lse(q.float().cpu(), k.float().cpu(), v.float().cpu(), scale,
                                c["off"], window=c["window"])
     if c["merged"]:
-        po = randn(gen, (tq, h, d), dtype).to(dev)
+        # a partial output at the same half scale
+        po = (randn(gen, (tq, h, d), torch.float32) * 0.5).to(dtype).to(dev)
         pl = (torch.randn(h, tq, generator=gen) * 3).to(dev)
         lse = torch.empty(h, tq, dtype=torch.float32, device=dev)
         out = ring_attn_merged(q, k, v, scale, c["off"], po, pl, window=c["window"],
